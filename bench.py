@@ -1,0 +1,347 @@
+"""Benchmark of the DSA sparse-MLA hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3]
+
+A "step" is one sparse-MLA decode call over one batch of synthetic inputs that
+are already resident in HBM.  Default workload: BASELINE config 3 (the one the
+north-star target is quoted on) - fp8 656-byte KV rows, batch 128, MTP s_q = 2,
+128 heads, top-k 2048, seq_len 65536 paged at 64 rows, causal.  The JSON line
+also carries config 5 (bf16 sparse prefill, 8192 x 128 heads x top-k 2048) in
+TFLOP/s, the dominant kernel's roofline, and the CPU oracle timed on a bounded
+sample of the same workload on this host.
+
+Algorithmic work (V = valid (query, index) pairs):
+  FLOPs = 2 * 128 * (576 + 512) * V
+  bytes = Q + V * row_bytes + O + LSE + indices   (row_bytes 656 fp8 / 1152 bf16)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+H, D_QK, D_VO = 128, 576, 512
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+SM_SCALE = 1.0 / math.sqrt(192.0)
+FLOP_PER_PAIR = 2 * H * (D_QK + D_VO)
+
+CONFIGS = {
+    "c1": dict(kind="decode", B=2, s_q=1, seq=8192, block=None, topk=2048, pad=256, fp8=False,
+               causal=False),
+    "c2": dict(kind="decode", B=64, s_q=1, seq=32768, block=64, topk=2048, pad=0, fp8=False,
+               causal=False),
+    "c3": dict(kind="decode", B=128, s_q=2, seq=65536, block=64, topk=2048, pad=0, fp8=True,
+               causal=True),
+    "c4": dict(kind="decode", B=4, s_q=1, seq=None, block=64, topk=2048, pad=0, fp8=False,
+               causal=False, splits=8),
+    "c5": dict(kind="prefill", N=8192, topk=2048),
+}
+NAMES = {
+    "c1": "bf16 sparse MLA decode B=2 H=128 top-k 2048 (256 pad) flat KV 8192",
+    "c2": "bf16 sparse MLA decode B=64 H=128 top-k 2048 paged(64) seq 32768",
+    "c3": "fp8-KV(656B) sparse MLA decode B=128 s_q=2 (MTP) H=128 top-k 2048 paged(64) seq 65536 causal",
+    "c4": "bf16 split-top-k decode B=4 H=128 top-k<=2048 seq U[1024,131072] 8 splits + combine",
+    "c5": "bf16 sparse MLA prefill N=8192 H=128 top-k 2048 from [0,t]",
+}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ inputs
+
+def make_decode(cfg, dev, seed=2026):
+    import torch
+    from opfoundry_amd import dsa
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    B, s_q, topk = cfg["B"], cfg["s_q"], cfg["topk"]
+    if cfg["seq"] is None:   # config 4: seq_lens ~ U[1024, 131072]
+        seq_lens = torch.randint(1024, 131073, (B,), generator=g, device=dev, dtype=torch.int32)
+    else:
+        seq_lens = torch.full((B,), cfg["seq"], dtype=torch.int32, device=dev)
+    max_len = int(seq_lens.max())
+    q = torch.randn((B, s_q, H, D_QK), generator=g, device=dev).to(torch.bfloat16)
+    bs = cfg["block"]
+    if bs:
+        mb = (max_len + bs - 1) // bs
+        nblk = B * mb
+        rows = nblk * bs
+        block_table = torch.randperm(nblk, generator=g, device=dev).to(torch.int32).view(B, mb)
+    else:
+        rows = B * max_len
+        block_table = None
+    # latent rows ~N(0,1): bf16 cache directly, or quantised by the fp8 cache writer
+    if cfg["fp8"]:
+        kv = torch.empty((rows, 656), dtype=torch.uint8, device=dev)
+        chunk = 1 << 20
+        for r0 in range(0, rows, chunk):
+            n = min(chunk, rows - r0)
+            src = torch.randn((n, D_QK), generator=g, device=dev).to(torch.bfloat16)
+            dsa.quantize_kv_fp8(src, kv[r0:r0 + n])
+    else:
+        kv = torch.randn((rows, D_QK), generator=g, device=dev).to(torch.bfloat16)
+    # distinct top-k positions per query token (scattered order), causal bound, -1 padding
+    idx = torch.full((B, s_q, topk), -1, dtype=torch.int32, device=dev)
+    for b in range(B):
+        L = int(seq_lens[b])
+        for t in range(s_q):
+            hi = L - s_q + t + 1 if cfg["causal"] else L
+            n = min(topk - cfg["pad"], hi)
+            r = torch.rand((hi,), generator=g, device=dev)
+            idx[b, t, :n] = torch.topk(r, n).indices.to(torch.int32)
+    torch.cuda.synchronize()
+    return dict(q=q, kv=kv, idx=idx, seq_lens=seq_lens, block_table=block_table, block_size=bs or 1,
+                kv_batch_stride=0 if bs else max_len, causal=cfg["causal"])
+
+
+def decode_call(d, splits=0, out=None, lse=None, ws=None):
+    from opfoundry_amd import dsa
+    return dsa.mla_decode(d["q"], d["kv"], d["idx"], SM_SCALE, out, lse, seq_lens=d["seq_lens"],
+                          block_table=d["block_table"], block_size=d["block_size"],
+                          causal=d["causal"], num_splits=splits,
+                          kv_batch_stride=d["kv_batch_stride"], workspace=ws)
+
+
+def make_prefill(cfg, dev, seed=2031):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    N, topk = cfg["N"], cfg["topk"]
+    q = torch.randn((N, H, D_QK), generator=g, device=dev).to(torch.bfloat16)
+    kv = torch.randn((N, D_QK), generator=g, device=dev).to(torch.bfloat16)
+    idx = torch.empty((N, topk), dtype=torch.int32, device=dev)
+    for r0 in range(0, N, 1024):
+        n = min(1024, N - r0)
+        r = torch.rand((n, N), generator=g, device=dev)
+        t = torch.arange(r0, r0 + n, device=dev)[:, None]
+        col = torch.arange(N, device=dev)[None, :]
+        r = torch.where(col <= t, r, torch.full_like(r, -1.0))
+        v, i = torch.topk(r, topk, dim=1)
+        idx[r0:r0 + n] = torch.where(v >= 0, i, torch.full_like(i, -1)).to(torch.int32)
+    torch.cuda.synchronize()
+    return dict(q=q, kv=kv, idx=idx)
+
+
+def count_valid(d) -> int:
+    import torch
+    idx = d["idx"].long()
+    if "seq_lens" not in d:
+        return int((idx >= 0).sum())
+    B, s_q, _ = idx.shape
+    L = d["seq_lens"].long().view(B, 1, 1)
+    hi = L - s_q + torch.arange(s_q, device=idx.device).view(1, s_q, 1) + 1 if d["causal"] else L
+    return int(((idx >= 0) & (idx < torch.minimum(L, hi))).sum())
+
+
+# ------------------------------------------------------------------ timing
+
+def time_steps(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps  # ms per step
+
+
+def kernel_avg_ms(fn, reps):
+    """Average duration of one launch of the dominant kernel, from HIP events recorded on the
+    stream the kernel is launched on (torch's current stream), one event pair per launch."""
+    import torch
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(reps)]
+    torch.cuda.synchronize()
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / reps
+
+
+# -------------------------------------------------------------- CPU baseline
+
+def cpu_baseline_decode(d, fmt_fp8, sample_queries, unit_scale):
+    """Time the C oracle on `sample_queries` query tokens of the same workload (their rows
+    gathered into a compact cache, indices remapped), scaled to the full step."""
+    import numpy as np
+    import torch
+    import oracle
+    B, s_q, topk = d["idx"].shape
+    picks = [(b, t) for b in range(B) for t in range(s_q)][:sample_queries]
+    qs, rows, idxs = [], [], []
+    for n, (b, t) in enumerate(picks):
+        qs.append(d["q"][b, t])
+        ii = d["idx"][b, t].long()
+        L = int(d["seq_lens"][b])
+        hi = L - s_q + t + 1 if d["causal"] else L
+        ok = (ii >= 0) & (ii < min(L, hi))
+        j = ii.clamp(min=0)
+        if d["block_table"] is not None:
+            bs = d["block_size"]
+            phys = d["block_table"][b].long()[j // bs] * bs + j % bs
+        else:
+            phys = b * d["kv_batch_stride"] + j
+        rows.append(d["kv"][phys])
+        loc = torch.arange(topk, device=ii.device) + n * topk
+        idxs.append(torch.where(ok, loc, torch.full_like(loc, -1)))
+    q = torch.stack(qs).view(len(picks), 1, H, D_QK).cpu().view(torch.int16).numpy().view(np.uint16)
+    kv = torch.cat(rows).cpu()
+    kv = kv.numpy() if fmt_fp8 else kv.view(torch.int16).numpy().view(np.uint16)
+    idx = torch.stack(idxs).view(len(picks), 1, topk).to(torch.int32).cpu().numpy()
+    sl = np.full(len(picks), kv.shape[0], np.int32)
+    nt = oracle.num_threads()
+    t0 = time.perf_counter()
+    oracle.mla_decode(q, kv, idx, sl, SM_SCALE, num_threads=nt)
+    dt = time.perf_counter() - t0
+    per_query = dt / len(picks)
+    return dict(value=per_query * unit_scale * 1e6, unit="us/step", cores=nt, kind="port",
+                sample=f"{len(picks)} of {B * s_q} query tokens (all 128 heads, full top-k), "
+                       f"{dt:.2f} s measured, scaled x{unit_scale / len(picks):.1f} to one step")
+
+
+def cpu_baseline_prefill(p, sample_queries, total_pairs):
+    import numpy as np
+    import torch
+    import oracle
+    N = p["q"].shape[0]
+    sel = torch.linspace(N // 2, N - 1, sample_queries).long()
+    q = p["q"][sel].cpu().view(torch.int16).numpy().view(np.uint16)
+    kv = p["kv"].cpu().view(torch.int16).numpy().view(np.uint16)
+    idx = p["idx"][sel].cpu().numpy()
+    pairs = int((p["idx"][sel] >= 0).sum())
+    nt = oracle.num_threads()
+    t0 = time.perf_counter()
+    oracle.mla_prefill(q, kv, idx, SM_SCALE, num_threads=nt)
+    dt = time.perf_counter() - t0
+    tflops = FLOP_PER_PAIR * pairs / dt / 1e12
+    return dict(value=tflops, unit="TFLOP/s", cores=nt, kind="port",
+                sample=f"{sample_queries} of {N} queries ({pairs} pairs), {dt:.2f} s; "
+                       f"full step would take {dt * total_pairs / pairs:.0f} s")
+
+
+# --------------------------------------------------------------------- main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c3", choices=[k for k in CONFIGS if k != "c5"])
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-sample", type=int, default=4)
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only run the timed decode steps (for profiler runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); "
+              "multi-GPU runs are not part of this build", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from opfoundry_amd.abi import load_library
+    load_library()
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[args.config]
+
+    log(f"building {args.config} inputs")
+    d = make_decode(cfg, dev)
+    splits = cfg.get("splits", 0)
+    out, lse = decode_call(d, splits)
+    from opfoundry_amd import dsa
+    a = dsa.make_decode_args(d["q"], d["kv"], d["idx"], SM_SCALE, out, lse, seq_lens=d["seq_lens"],
+                             block_table=d["block_table"], block_size=d["block_size"],
+                             causal=d["causal"], num_splits=splits,
+                             kv_batch_stride=d["kv_batch_stride"])
+    ns = dsa.decode_num_splits(a)
+    ws_bytes = dsa.decode_workspace_size(a)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    step = lambda: decode_call(d, splits, out, lse, ws)  # noqa: E731
+
+    log(f"timing {args.steps} steps after {args.warmup} warm-up (splits={ns})")
+    ms = time_steps(step, args.steps, args.warmup)
+    if args.kernel_only:
+        print(json.dumps({"config": args.config, "ms_per_step": ms}))
+        return
+
+    B, s_q, topk = d["idx"].shape
+    V = count_valid(d)
+    row_bytes = 656 if cfg["fp8"] else 1152
+    alg_bytes = (B * s_q * H * D_QK * 2 + V * row_bytes + B * s_q * H * D_VO * 2 + B * s_q * H * 4
+                 + B * s_q * topk * 4)
+    flops = FLOP_PER_PAIR * V
+    # dominant kernel: the fused decode kernel (the only one when unsplit)
+    k_ms = kernel_avg_ms(step, max(10, args.steps // 2)) if ns == 1 else None
+    dom_ms = k_ms if k_ms is not None else ms
+    achieved = alg_bytes / (dom_ms * 1e-3) / 1e9
+    res = {
+        "metric": "sparse-MLA decode us/step + achieved HBM TB/s; prefill TFLOP/s (1 MI355X)",
+        "value": round(ms * 1e3, 3),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"{args.config}: {NAMES[args.config]}", "kv_format":
+                   "fp8_e4m3_656B" if cfg["fp8"] else "bf16_1152B", "num_splits": ns,
+                   "valid_pairs": V, "parallelism": "none (1 GPU)"},
+        "hbm_TBps": round(alg_bytes / (ms * 1e-3) / 1e12, 3),
+        "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "dsa_mla_fwd_kernel<fp8>" if cfg["fp8"] else "dsa_mla_fwd_kernel<bf16>",
+                     "kernel_avg_us": round(dom_ms * 1e3, 3), "alg_bytes": alg_bytes,
+                     "mfma_frac": round(flops / (dom_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)},
+    }
+    del out, lse, ws
+
+    if not args.no_cpu:
+        log("CPU baseline (oracle) on a bounded sample")
+        res["cpu_baseline"] = cpu_baseline_decode(d, cfg["fp8"], args.cpu_sample, B * s_q)
+    del d
+    torch.cuda.empty_cache()
+
+    if not args.no_prefill:
+        log("building c5 prefill inputs")
+        p = make_prefill(CONFIGS["c5"], dev)
+        pout = torch.empty((p["q"].shape[0], H, D_VO), dtype=torch.bfloat16, device=dev)
+        plse = torch.empty((p["q"].shape[0], H), dtype=torch.float32, device=dev)
+        pstep = lambda: dsa.mla_prefill(p["q"], p["kv"], p["idx"], SM_SCALE, pout, plse)  # noqa
+        psteps = max(3, args.steps // 5)
+        pms = time_steps(pstep, psteps, 2)
+        pV = int((p["idx"] >= 0).sum())
+        pfl = FLOP_PER_PAIR * pV
+        res["prefill"] = {"workload": f"c5: {NAMES['c5']}", "ms_per_step": round(pms, 4),
+                          "tflops": round(pfl / (pms * 1e-3) / 1e12, 1), "valid_pairs": pV,
+                          "roofline": {"bound": "mfma", "achieved": round(pfl / (pms * 1e-3) / 1e12, 1),
+                                       "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                       "frac": round(pfl / (pms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}}
+        if not args.no_cpu:
+            res["prefill"]["cpu_baseline"] = cpu_baseline_prefill(p, 4, pV)
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,207 @@
+/*
+ * dsa_mla.h - C ABI of the MI355X (gfx950) DeepSeek sparse-attention (DSA)
+ * MLA decode / prefill library, libdsa_mla.so.
+ *
+ * One latent KV row is 576 values: 512 "NoPE" values (which are also the
+ * value vector V) followed by 64 "RoPE" values.  Every query head attends
+ * the same gathered rows; the output is 512 wide per head.
+ *
+ * Row formats in the KV cache (byte layout of one cache row):
+ *   DSA_KV_BF16    : 576 x bf16                                  = 1152 B
+ *   DSA_KV_FP8_656 : [0,512)   512 x fp8 e4m3fn NoPE codes
+ *                    [512,528) 4 x fp32 scales, scale g covers NoPE dims
+ *                              [128g, 128g+128) and equals amax_g / 448
+ *                    [528,656) 64 x bf16 RoPE                    =  656 B
+ *   Dequantised value of NoPE dim d = float(e4m3(code_d)) * scale[d / 128].
+ *
+ * Index semantics (top-k form).  indices[b][t][k] is a logical position j in
+ * sequence b.  It is valid iff 0 <= j < seq_lens[b] and, when causal != 0,
+ * j <= seq_lens[b] - s_q + t.  Invalid entries (-1 padding included)
+ * contribute nothing.  The physical cache row of a valid j is
+ *   block_table[b * block_table_stride + j / block_size] * block_size
+ *       + j % block_size                       (block_table != NULL)
+ *   b * kv_batch_stride + j                    (block_table == NULL)
+ * and a physical row outside [0, kv_total_rows) is treated as invalid, so a
+ * bad block table can never make a kernel read outside the cache.
+ * Duplicated positions count once per occurrence.  A (b, t, head) with no
+ * valid entry gets O = 0 and LSE = +inf.
+ *
+ * Numerics.  Scores s = (q . k) * sm_scale in fp32; softmax probabilities are
+ * rounded to bf16 before the P.V product, accumulation is fp32, O is written
+ * as bf16 (round to nearest even) and LSE = max + ln(sum exp(s - max)) as
+ * fp32 (natural log of the scaled scores).
+ *
+ * Conventions.  All pointers are device pointers owned by the caller (the
+ * workspace included); strides are in elements; `stream` is a hipStream_t
+ * (NULL = the null stream).  Every entry point validates its arguments
+ * before any launch and returns 0 on success or a negative DSA_ERR_* code;
+ * nothing calls exit().  The library holds no mutable global state, so calls
+ * on distinct streams with distinct workspaces may run concurrently.
+ */
+#ifndef DSA_MLA_H_
+#define DSA_MLA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSA_MLA_D_QK 576
+#define DSA_MLA_D_NOPE 512
+#define DSA_MLA_D_ROPE 64
+#define DSA_MLA_D_VO 512
+#define DSA_MLA_FP8_ROW_BYTES 656
+#define DSA_MLA_BF16_ROW_BYTES 1152
+#define DSA_MLA_MAX_SPLITS 64
+
+typedef enum {
+    DSA_KV_BF16 = 0,
+    DSA_KV_FP8_656 = 1
+} dsa_kv_format;
+
+enum {
+    DSA_OK = 0,
+    DSA_ERR_NULL_POINTER = -1,
+    DSA_ERR_BAD_SHAPE = -2,
+    DSA_ERR_UNSUPPORTED = -3,
+    DSA_ERR_BAD_FORMAT = -4,
+    DSA_ERR_WORKSPACE = -5,
+    DSA_ERR_BAD_SPLITS = -6,
+    DSA_ERR_BAD_STRIDE = -7,
+    DSA_ERR_HIP = -8
+};
+
+/*
+ * Sparse MLA decode, top-k form.
+ * q       : bf16 [B, s_q, H, 576] addressed by q_stride_{b,t,h} (last dim dense)
+ * kv_cache: [kv_total_rows, row] in kv_format; rows are block_size-row pages
+ * out     : bf16 [B, s_q, H, 512] addressed by o_stride_{b,t,h}
+ * lse     : fp32 [B, s_q, H] dense (may be NULL)
+ * num_splits: 0 = automatic; otherwise 1..DSA_MLA_MAX_SPLITS.  With more than
+ *           one split the top-k list of every query token is cut into
+ *           num_splits contiguous chunks whose partial results (fp32 O and
+ *           LSE, kept in the workspace) are merged by the combine kernel.
+ */
+typedef struct {
+    const void* q;
+    int64_t q_stride_b, q_stride_t, q_stride_h;
+
+    const void* kv_cache;
+    int64_t kv_total_rows;
+    int32_t kv_format;
+    int32_t block_size;
+    int64_t kv_batch_stride;
+
+    const int32_t* block_table;
+    int64_t block_table_stride;
+
+    const int32_t* seq_lens;
+
+    const int32_t* indices;
+    int64_t idx_stride_b, idx_stride_t;
+
+    void* out;
+    int64_t o_stride_b, o_stride_t, o_stride_h;
+    float* lse;
+
+    int32_t B, s_q, H, topk;
+    int32_t num_splits;
+    int32_t causal;
+    float sm_scale;
+} dsa_mla_decode_args;
+
+/*
+ * Workspace bytes dsa_mla_decode needs for these arguments (0 when the call
+ * runs unsplit).  Replaces the buffer sizing of mla_decode_plan_create,
+ * opus_attn/dsa_v32/common/host.cc:151-178.
+ */
+int dsa_mla_decode_workspace_size(const dsa_mla_decode_args* args, size_t* bytes);
+
+/*
+ * Number of splits dsa_mla_decode uses for these arguments (resolves
+ * num_splits == 0).  Pure host function.
+ */
+int dsa_mla_decode_num_splits(const dsa_mla_decode_args* args, int32_t* num_splits);
+
+/*
+ * Launch the decode pipeline on `stream`: the fused gather / QK / softmax /
+ * PV kernel, followed by the split combine when more than one split is used.
+ * Replaces mla_decode_launch_pipeline, opus_attn/dsa_v32/common/host.cc:114-138
+ * (metadata -> decode -> reduce); the kernel argument block it builds carries
+ * the fields of opus_mla_decode_kargs, opus_attn/dsa_v32/common/defs.h:109-131.
+ */
+int dsa_mla_decode(const dsa_mla_decode_args* args, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/*
+ * Merge split partials: partial_o fp32 [num_splits, rows, H, 512] (each split
+ * normalised by its own softmax sum), partial_lse fp32 [num_splits, rows, H]
+ * (natural log; -FLT_MAX marks an empty split) into out bf16 (row stride
+ * o_stride_row, head stride o_stride_h, elements) and lse fp32 [rows, H]
+ * (may be NULL).  rows = B * s_q.  Replaces mla_reduce_kernel,
+ * opus_attn/dsa_v32/common/mla_reduce.hpp:158-184.
+ */
+int dsa_mla_combine(const float* partial_o, const float* partial_lse, int32_t num_splits,
+                    int32_t rows, int32_t H, void* out, int64_t o_stride_row, int64_t o_stride_h,
+                    float* lse, void* stream);
+
+/*
+ * Sparse MLA prefill (per-query top-k over one KV pool).
+ * q       : bf16 [N, H, 576] addressed by q_stride_{n,h}
+ * kv      : [kv_rows, row] in kv_format
+ * indices : int32 [N, topk] (row stride idx_stride_n); entry j of query i is
+ *           valid iff 0 <= j < kv_rows and, when causal != 0,
+ *           j <= i + causal_offset
+ * out     : bf16 [N, H, 512]; lse fp32 [N, H] (may be NULL)
+ * Replaces mla_v4_prefill_launch, opus_attn/dsa_v4/common/mla_v4_host.cc:28-47,
+ * with the V3.2 shape (576 / 512), no attention sink, and an LSE output.
+ */
+typedef struct {
+    const void* q;
+    int64_t q_stride_n, q_stride_h;
+    const void* kv;
+    int64_t kv_rows;
+    int32_t kv_format;
+    const int32_t* indices;
+    int64_t idx_stride_n;
+    void* out;
+    int64_t o_stride_n, o_stride_h;
+    float* lse;
+    int32_t N, H, topk;
+    int32_t causal;
+    int64_t causal_offset;
+    float sm_scale;
+} dsa_mla_prefill_args;
+
+int dsa_mla_prefill_workspace_size(const dsa_mla_prefill_args* args, size_t* bytes);
+int dsa_mla_prefill(const dsa_mla_prefill_args* args, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/*
+ * fp8 cache writer: quantise n_rows bf16 latent rows (576 values, row stride
+ * src_stride elements) into 656-byte DSA_KV_FP8_656 rows.  Destination row
+ * of source row r is dst_rows[r] (int64 physical cache row) or r when
+ * dst_rows is NULL; negative destinations are skipped.  scale_g =
+ * amax_g / 448 (IEEE division), code = e4m3fn(x / scale_g) with round to
+ * nearest even and saturation to +-448; an all-zero group stores scale 0 and
+ * zero codes.  The reference leaves cache writing to its caller
+ * (opus_attn/dsa_v32/README.md:99); the codec follows float_to_fp8_e4m3,
+ * opus_attn/dsa_v32/common/defs.h:11-38.
+ */
+int dsa_kv_quantize_fp8(const void* src_bf16, int64_t src_stride, int64_t n_rows,
+                        void* dst_cache, int64_t dst_total_rows, const int64_t* dst_rows,
+                        void* stream);
+
+/* Human-readable text for a DSA_ERR_* code. */
+const char* dsa_mla_strerror(int code);
+
+/* ABI version, bumped on any change of the argument structs. */
+int dsa_mla_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_MLA_H_ */

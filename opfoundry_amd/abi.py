@@ -1,0 +1,135 @@
+"""ctypes mirror of include/dsa_mla.h and the loader of libdsa_mla.so.
+
+The library is the product: every call in :mod:`opfoundry_amd.dsa` goes
+through it.  There is no CPU fallback - if the shared object is missing the
+loader raises, so a GPU run can never silently compute elsewhere.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "_build", "libdsa_mla.so")
+
+D_QK, D_NOPE, D_ROPE, D_VO = 576, 512, 64, 512
+FP8_ROW_BYTES, BF16_ROW_BYTES = 656, 1152
+MAX_SPLITS = 64
+
+KV_BF16 = 0
+KV_FP8_656 = 1
+
+DSA_OK = 0
+ERRORS = {
+    -1: "DSA_ERR_NULL_POINTER",
+    -2: "DSA_ERR_BAD_SHAPE",
+    -3: "DSA_ERR_UNSUPPORTED",
+    -4: "DSA_ERR_BAD_FORMAT",
+    -5: "DSA_ERR_WORKSPACE",
+    -6: "DSA_ERR_BAD_SPLITS",
+    -7: "DSA_ERR_BAD_STRIDE",
+    -8: "DSA_ERR_HIP",
+}
+
+# Every symbol include/dsa_mla.h declares, in declaration order.
+EXPORTED_SYMBOLS = (
+    "dsa_mla_decode_workspace_size",
+    "dsa_mla_decode_num_splits",
+    "dsa_mla_decode",
+    "dsa_mla_combine",
+    "dsa_mla_prefill_workspace_size",
+    "dsa_mla_prefill",
+    "dsa_kv_quantize_fp8",
+    "dsa_mla_strerror",
+    "dsa_mla_abi_version",
+)
+
+ABI_VERSION = 1
+
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_vp = ctypes.c_void_p
+
+
+class DecodeArgs(ctypes.Structure):
+    """dsa_mla_decode_args (include/dsa_mla.h)."""
+
+    _fields_ = [
+        ("q", _vp), ("q_stride_b", _i64), ("q_stride_t", _i64), ("q_stride_h", _i64),
+        ("kv_cache", _vp), ("kv_total_rows", _i64), ("kv_format", _i32), ("block_size", _i32),
+        ("kv_batch_stride", _i64),
+        ("block_table", _vp), ("block_table_stride", _i64),
+        ("seq_lens", _vp),
+        ("indices", _vp), ("idx_stride_b", _i64), ("idx_stride_t", _i64),
+        ("out", _vp), ("o_stride_b", _i64), ("o_stride_t", _i64), ("o_stride_h", _i64),
+        ("lse", _vp),
+        ("B", _i32), ("s_q", _i32), ("H", _i32), ("topk", _i32),
+        ("num_splits", _i32), ("causal", _i32), ("sm_scale", ctypes.c_float),
+    ]
+
+
+class PrefillArgs(ctypes.Structure):
+    """dsa_mla_prefill_args (include/dsa_mla.h)."""
+
+    _fields_ = [
+        ("q", _vp), ("q_stride_n", _i64), ("q_stride_h", _i64),
+        ("kv", _vp), ("kv_rows", _i64), ("kv_format", _i32),
+        ("indices", _vp), ("idx_stride_n", _i64),
+        ("out", _vp), ("o_stride_n", _i64), ("o_stride_h", _i64),
+        ("lse", _vp),
+        ("N", _i32), ("H", _i32), ("topk", _i32), ("causal", _i32),
+        ("causal_offset", _i64), ("sm_scale", ctypes.c_float),
+    ]
+
+
+class DsaError(RuntimeError):
+    def __init__(self, code: int, where: str):
+        self.code = code
+        super().__init__(f"{where} failed: {ERRORS.get(code, code)} ({_strerror(code)})")
+
+
+_LIB = None
+
+
+def load_library(path: str | None = None) -> ctypes.CDLL:
+    """Load libdsa_mla.so (built by opfoundry_amd.build); raise if it is absent."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    p = path or LIB_PATH
+    if not os.path.exists(p):
+        raise RuntimeError(
+            f"libdsa_mla.so not found at {p}: build it with `python -m opfoundry_amd.build` "
+            "(there is no CPU fallback)")
+    lib = ctypes.CDLL(p)
+    sz = ctypes.POINTER(ctypes.c_size_t)
+    lib.dsa_mla_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeArgs), sz]
+    lib.dsa_mla_decode_num_splits.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.POINTER(_i32)]
+    lib.dsa_mla_decode.argtypes = [ctypes.POINTER(DecodeArgs), _vp, ctypes.c_size_t, _vp]
+    lib.dsa_mla_combine.argtypes = [_vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _vp]
+    lib.dsa_mla_prefill_workspace_size.argtypes = [ctypes.POINTER(PrefillArgs), sz]
+    lib.dsa_mla_prefill.argtypes = [ctypes.POINTER(PrefillArgs), _vp, ctypes.c_size_t, _vp]
+    lib.dsa_kv_quantize_fp8.argtypes = [_vp, _i64, _i64, _vp, _i64, _vp, _vp]
+    lib.dsa_mla_strerror.argtypes = [ctypes.c_int]
+    lib.dsa_mla_strerror.restype = ctypes.c_char_p
+    lib.dsa_mla_abi_version.argtypes = []
+    for name in EXPORTED_SYMBOLS:
+        if name not in ("dsa_mla_strerror",):
+            getattr(lib, name).restype = ctypes.c_int
+    if lib.dsa_mla_abi_version() != ABI_VERSION:
+        raise RuntimeError("libdsa_mla.so ABI version mismatch; rebuild it")
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+def _strerror(code: int) -> str:
+    try:
+        return load_library().dsa_mla_strerror(code).decode()
+    except Exception:  # the library itself may be what is missing
+        return ERRORS.get(code, "unknown")
+
+
+def check(code: int, where: str) -> None:
+    if code != DSA_OK:
+        raise DsaError(code, where)

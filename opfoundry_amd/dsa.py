@@ -1,0 +1,223 @@
+"""Torch-facing host API of the DSA sparse-MLA library.
+
+These functions mirror the reference's launch API for the path - q, latent KV
+cache, top-k index tensor, sm_scale, output and LSE
+(``mla_decode_launch_pipeline``, opus_attn/dsa_v32/common/host.cc:114-138;
+``mla_v4_prefill_launch``, opus_attn/dsa_v4/common/mla_v4_host.cc:28-47) -
+and forward to the C ABI of libdsa_mla.so.  PyTorch only provides device
+memory and the current stream; all compute happens in the HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from . import abi
+from .abi import DecodeArgs, PrefillArgs, check, load_library
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+def kv_format_of(kv: torch.Tensor) -> Tuple[int, int]:
+    """(kv_format, total_rows) of a cache tensor: bf16 [..., 576] or uint8 [..., 656]."""
+    if kv.dtype == torch.bfloat16 and kv.shape[-1] == abi.D_QK:
+        return abi.KV_BF16, kv.numel() // abi.D_QK
+    if kv.dtype == torch.uint8 and kv.shape[-1] == abi.FP8_ROW_BYTES:
+        return abi.KV_FP8_656, kv.numel() // abi.FP8_ROW_BYTES
+    raise ValueError(f"kv cache must be bf16 [..., 576] or uint8 [..., 656], got {kv.dtype} "
+                     f"{tuple(kv.shape)}")
+
+
+def _need(t: torch.Tensor, dtype, name: str):
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+
+
+def make_decode_args(q, kv_cache, indices, sm_scale, out, lse, *, seq_lens, block_table=None,
+                     block_size=None, causal=False, num_splits=0, kv_batch_stride=0):
+    B, s_q, H, D = q.shape
+    if D != abi.D_QK or q.stride(3) != 1:
+        raise ValueError("q must be [B, s_q, H, 576] with a dense last dim")
+    if tuple(indices.shape[:2]) != (B, s_q) or indices.stride(2) != 1:
+        raise ValueError("indices must be [B, s_q, topk] with a dense last dim")
+    fmt, rows = kv_format_of(kv_cache)
+    if block_table is not None:
+        if block_size is None:
+            block_size = kv_cache.shape[-2] if kv_cache.dim() >= 3 else None
+        if block_size is None:
+            raise ValueError("block_size is required with a block table")
+        bt_stride = block_table.stride(0)
+    else:
+        block_size = block_size or 1
+        bt_stride = 0
+    a = DecodeArgs()
+    a.q = _ptr(q)
+    a.q_stride_b, a.q_stride_t, a.q_stride_h = q.stride(0), q.stride(1), q.stride(2)
+    a.kv_cache = _ptr(kv_cache)
+    a.kv_total_rows = rows
+    a.kv_format = fmt
+    a.block_size = int(block_size)
+    a.kv_batch_stride = int(kv_batch_stride)
+    a.block_table = _ptr(block_table)
+    a.block_table_stride = bt_stride
+    a.seq_lens = _ptr(seq_lens)
+    a.indices = _ptr(indices)
+    a.idx_stride_b, a.idx_stride_t = indices.stride(0), indices.stride(1)
+    a.out = _ptr(out)
+    a.o_stride_b, a.o_stride_t, a.o_stride_h = out.stride(0), out.stride(1), out.stride(2)
+    a.lse = _ptr(lse)
+    a.B, a.s_q, a.H, a.topk = B, s_q, H, indices.shape[2]
+    a.num_splits = int(num_splits)
+    a.causal = 1 if causal else 0
+    a.sm_scale = float(sm_scale)
+    return a
+
+
+def decode_workspace_size(args: DecodeArgs) -> int:
+    n = ctypes.c_size_t(0)
+    check(load_library().dsa_mla_decode_workspace_size(ctypes.byref(args), ctypes.byref(n)),
+          "dsa_mla_decode_workspace_size")
+    return n.value
+
+
+def decode_num_splits(args: DecodeArgs) -> int:
+    n = ctypes.c_int32(0)
+    check(load_library().dsa_mla_decode_num_splits(ctypes.byref(args), ctypes.byref(n)),
+          "dsa_mla_decode_num_splits")
+    return n.value
+
+
+def mla_decode(q: torch.Tensor, kv_cache: torch.Tensor, indices: torch.Tensor, sm_scale: float,
+               out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None, *,
+               seq_lens: torch.Tensor, block_table: Optional[torch.Tensor] = None,
+               block_size: Optional[int] = None, causal: bool = False, num_splits: int = 0,
+               kv_batch_stride: int = 0, workspace: Optional[torch.Tensor] = None,
+               stream=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Sparse MLA decode over a (paged) latent cache; returns (out bf16, lse fp32).
+
+    q [B, s_q, H, 576] bf16; kv_cache bf16 [..., 576] or uint8 [..., 656]
+    (fp8 e4m3 + per-128 scales + bf16 RoPE); indices int32 [B, s_q, topk]
+    with -1 padding; seq_lens int32 [B]; block_table int32 [B, max_blocks].
+    """
+    _need(q, torch.bfloat16, "q")
+    _need(indices, torch.int32, "indices")
+    _need(seq_lens, torch.int32, "seq_lens")
+    if block_table is not None:
+        _need(block_table, torch.int32, "block_table")
+    B, s_q, H, _ = q.shape
+    if out is None:
+        out = torch.empty((B, s_q, H, abi.D_VO), dtype=torch.bfloat16, device=q.device)
+    if lse is None:
+        lse = torch.empty((B, s_q, H), dtype=torch.float32, device=q.device)
+    a = make_decode_args(q, kv_cache, indices, sm_scale, out, lse, seq_lens=seq_lens,
+                         block_table=block_table, block_size=block_size, causal=causal,
+                         num_splits=num_splits, kv_batch_stride=kv_batch_stride)
+    ws_bytes = decode_workspace_size(a)
+    if ws_bytes and (workspace is None or workspace.numel() * workspace.element_size() < ws_bytes):
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    check(load_library().dsa_mla_decode(ctypes.byref(a), _ptr(workspace) if ws_bytes else None,
+                                        ws_bytes, _stream(stream)), "dsa_mla_decode")
+    return out, lse
+
+
+def mla_combine(partial_o: torch.Tensor, partial_lse: torch.Tensor,
+                out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
+                stream=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Merge split partials fp32 [S, rows, H, 512] + [S, rows, H] -> bf16 [rows, H, 512], lse."""
+    _need(partial_o, torch.float32, "partial_o")
+    _need(partial_lse, torch.float32, "partial_lse")
+    S, rows, H, D = partial_o.shape
+    if D != abi.D_VO or tuple(partial_lse.shape) != (S, rows, H):
+        raise ValueError("partial_o must be [S, rows, H, 512] and partial_lse [S, rows, H]")
+    if not (partial_o.is_contiguous() and partial_lse.is_contiguous()):
+        raise ValueError("partials must be contiguous")
+    if out is None:
+        out = torch.empty((rows, H, D), dtype=torch.bfloat16, device=partial_o.device)
+    if lse is None:
+        lse = torch.empty((rows, H), dtype=torch.float32, device=partial_o.device)
+    check(load_library().dsa_mla_combine(_ptr(partial_o), _ptr(partial_lse), S, rows, H, _ptr(out),
+                                         out.stride(0), out.stride(1), _ptr(lse), _stream(stream)),
+          "dsa_mla_combine")
+    return out, lse
+
+
+def make_prefill_args(q, kv, indices, sm_scale, out, lse, *, causal=False, causal_offset=0):
+    N, H, D = q.shape
+    if D != abi.D_QK or q.stride(2) != 1:
+        raise ValueError("q must be [N, H, 576] with a dense last dim")
+    if indices.shape[0] != N or indices.stride(1) != 1:
+        raise ValueError("indices must be [N, topk] with a dense last dim")
+    fmt, rows = kv_format_of(kv)
+    a = PrefillArgs()
+    a.q = _ptr(q)
+    a.q_stride_n, a.q_stride_h = q.stride(0), q.stride(1)
+    a.kv = _ptr(kv)
+    a.kv_rows = rows
+    a.kv_format = fmt
+    a.indices = _ptr(indices)
+    a.idx_stride_n = indices.stride(0)
+    a.out = _ptr(out)
+    a.o_stride_n, a.o_stride_h = out.stride(0), out.stride(1)
+    a.lse = _ptr(lse)
+    a.N, a.H, a.topk = N, H, indices.shape[1]
+    a.causal = 1 if causal else 0
+    a.causal_offset = int(causal_offset)
+    a.sm_scale = float(sm_scale)
+    return a
+
+
+def mla_prefill(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor, sm_scale: float,
+                out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None, *,
+                causal: bool = False, causal_offset: int = 0,
+                workspace: Optional[torch.Tensor] = None,
+                stream=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Sparse MLA prefill: per-query top-k over one KV pool; returns (out bf16, lse fp32)."""
+    _need(q, torch.bfloat16, "q")
+    _need(indices, torch.int32, "indices")
+    N, H, _ = q.shape
+    if out is None:
+        out = torch.empty((N, H, abi.D_VO), dtype=torch.bfloat16, device=q.device)
+    if lse is None:
+        lse = torch.empty((N, H), dtype=torch.float32, device=q.device)
+    a = make_prefill_args(q, kv, indices, sm_scale, out, lse, causal=causal,
+                          causal_offset=causal_offset)
+    n = ctypes.c_size_t(0)
+    lib = load_library()
+    check(lib.dsa_mla_prefill_workspace_size(ctypes.byref(a), ctypes.byref(n)),
+          "dsa_mla_prefill_workspace_size")
+    if n.value and (workspace is None or workspace.numel() * workspace.element_size() < n.value):
+        workspace = torch.empty(n.value, dtype=torch.uint8, device=q.device)
+    check(lib.dsa_mla_prefill(ctypes.byref(a), _ptr(workspace) if n.value else None, n.value,
+                              _stream(stream)), "dsa_mla_prefill")
+    return out, lse
+
+
+def quantize_kv_fp8(src: torch.Tensor, dst: Optional[torch.Tensor] = None,
+                    dst_rows: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Write bf16 latent rows [n, 576] into 656-byte fp8 cache rows (uint8 [rows, 656])."""
+    _need(src, torch.bfloat16, "src")
+    if src.shape[-1] != abi.D_QK or src.stride(-1) != 1:
+        raise ValueError("src must be [n, 576] bf16 with a dense last dim")
+    src2 = src.reshape(-1, abi.D_QK)
+    n = src2.shape[0]
+    if dst is None:
+        dst = torch.empty((n, abi.FP8_ROW_BYTES), dtype=torch.uint8, device=src.device)
+    _need(dst, torch.uint8, "dst")
+    if dst_rows is not None:
+        _need(dst_rows, torch.int64, "dst_rows")
+    check(load_library().dsa_kv_quantize_fp8(_ptr(src2), src2.stride(0), n, _ptr(dst),
+                                             dst.numel() // abi.FP8_ROW_BYTES, _ptr(dst_rows),
+                                             _stream(stream)), "dsa_kv_quantize_fp8")
+    return dst

@@ -1,0 +1,240 @@
+"""CPU oracle for the DSA sparse-MLA path - TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this package, and only as the checker (or the timed CPU baseline).  The
+product (opfoundry_amd) never imports or calls it.
+
+The arithmetic lives in oracle/dsa_oracle.c (built by oracle/Makefile into
+oracle/_build/libdsa_oracle.so); this module is its ctypes front end plus the
+seeded input generators the tests and the bench share.  Reference anchors for
+each C function are in that file's header.  Pinning: every function here is
+checked in tests/test_oracle_*.py against an independent statement of its
+answer (closed forms, brute force, torch's bf16 rounding, identities) - no
+function of the oracle is left "parity unpinned".
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+from opfoundry_amd.abi import D_QK, D_VO, DecodeArgs, KV_BF16, KV_FP8_656, PrefillArgs
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "libdsa_oracle.so")
+
+_LIB = None
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
+        L.oracle_f32_to_bf16.restype = ctypes.c_uint16
+        L.oracle_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.oracle_fp8_e4m3_encode.restype = ctypes.c_uint8
+        L.oracle_fp8_e4m3_encode.argtypes = [ctypes.c_float]
+        L.oracle_fp8_e4m3_decode.restype = ctypes.c_float
+        L.oracle_fp8_e4m3_decode.argtypes = [ctypes.c_uint8]
+        for n in ("oracle_fp8_encode_n", "oracle_fp8_decode_n", "oracle_bf16_round_n",
+                  "oracle_quantize_rows_656", "oracle_dequant_rows_656"):
+            getattr(L, n).argtypes = [vp, i64, vp] if "rows" in n else [vp, vp, i64]
+            getattr(L, n).restype = None
+        L.oracle_mla_decode.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.c_int]
+        L.oracle_mla_decode_partial.argtypes = [ctypes.POINTER(DecodeArgs), i32, i32, vp, vp,
+                                                ctypes.c_int]
+        L.oracle_mla_combine.argtypes = [vp, vp, i32, i64, i32, vp, vp]
+        L.oracle_mla_combine.restype = None
+        L.oracle_mla_prefill.argtypes = [ctypes.POINTER(PrefillArgs), ctypes.c_int]
+        L.oracle_num_threads.argtypes = [ctypes.c_int]
+        _LIB = L
+    return _LIB
+
+
+def _p(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data
+
+
+# ------------------------------------------------------------------ codecs
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bit patterns (uint16), round to nearest even."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().oracle_bf16_round_n(_p(x), _p(out), x.size)
+    return out
+
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def fp8_encode(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint8)
+    lib().oracle_fp8_encode_n(_p(x), _p(out), x.size)
+    return out
+
+
+def fp8_decode(c: np.ndarray) -> np.ndarray:
+    c = np.ascontiguousarray(c, dtype=np.uint8)
+    out = np.empty(c.shape, np.float32)
+    lib().oracle_fp8_decode_n(_p(c), _p(out), c.size)
+    return out
+
+
+def quantize_rows_656(rows_f32: np.ndarray) -> np.ndarray:
+    """[n, 576] fp32 (bf16-representable) -> [n, 656] uint8 cache rows."""
+    r = np.ascontiguousarray(rows_f32, dtype=np.float32).reshape(-1, D_QK)
+    out = np.empty((r.shape[0], 656), np.uint8)
+    lib().oracle_quantize_rows_656(_p(r), r.shape[0], _p(out))
+    return out
+
+
+def dequant_rows_656(rows: np.ndarray) -> np.ndarray:
+    r = np.ascontiguousarray(rows, dtype=np.uint8).reshape(-1, 656)
+    out = np.empty((r.shape[0], D_QK), np.float32)
+    lib().oracle_dequant_rows_656(_p(r), r.shape[0], _p(out))
+    return out
+
+
+# ------------------------------------------------------------- attention
+
+def _decode_args(q, kv, fmt, indices, seq_lens, block_table, block_size, kv_batch_stride, causal,
+                 sm_scale, out, lse):
+    B, s_q, H, _ = q.shape
+    a = DecodeArgs()
+    a.q = _p(q)
+    a.q_stride_b, a.q_stride_t, a.q_stride_h = s_q * H * D_QK, H * D_QK, D_QK
+    a.kv_cache = _p(kv)
+    a.kv_total_rows = kv.shape[0]
+    a.kv_format = fmt
+    a.block_size = block_size
+    a.kv_batch_stride = kv_batch_stride
+    a.block_table = _p(block_table)
+    a.block_table_stride = 0 if block_table is None else block_table.shape[1]
+    a.seq_lens = _p(seq_lens)
+    a.indices = _p(indices)
+    a.idx_stride_b, a.idx_stride_t = indices.shape[1] * indices.shape[2], indices.shape[2]
+    a.out = _p(out)
+    a.o_stride_b, a.o_stride_t, a.o_stride_h = s_q * H * D_VO, H * D_VO, D_VO
+    a.lse = _p(lse)
+    a.B, a.s_q, a.H, a.topk = B, s_q, H, indices.shape[2]
+    a.num_splits = 1
+    a.causal = 1 if causal else 0
+    a.sm_scale = float(sm_scale)
+    return a
+
+
+def _prep(q, kv, indices, seq_lens, block_table):
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    kv = np.ascontiguousarray(kv)
+    fmt = KV_BF16 if kv.dtype == np.uint16 else KV_FP8_656
+    if fmt == KV_BF16:
+        kv = kv.reshape(-1, D_QK)
+    else:
+        kv = kv.reshape(-1, 656)
+    indices = np.ascontiguousarray(indices, dtype=np.int32)
+    seq_lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    if block_table is not None:
+        block_table = np.ascontiguousarray(block_table, dtype=np.int32)
+    return q, kv, fmt, indices, seq_lens, block_table
+
+
+def mla_decode(q, kv, indices, seq_lens, sm_scale, *, block_table=None, block_size=1,
+               kv_batch_stride=0, causal=False, num_threads=0):
+    """Host oracle of dsa_mla_decode: q uint16(bf16) [B,s_q,H,576]; kv uint16 [rows,576]
+    (bf16) or uint8 [rows,656] (fp8); returns (O uint16 bf16 [B,s_q,H,512], LSE f32)."""
+    q, kv, fmt, indices, seq_lens, block_table = _prep(q, kv, indices, seq_lens, block_table)
+    B, s_q, H, _ = q.shape
+    out = np.zeros((B, s_q, H, D_VO), np.uint16)
+    lse = np.zeros((B, s_q, H), np.float32)
+    a = _decode_args(q, kv, fmt, indices, seq_lens, block_table, block_size, kv_batch_stride,
+                     causal, sm_scale, out, lse)
+    rc = lib().oracle_mla_decode(ctypes.byref(a), num_threads)
+    assert rc == 0
+    return out, lse
+
+
+def mla_decode_partial(q, kv, indices, seq_lens, sm_scale, k_begin, k_end, *, block_table=None,
+                       block_size=1, kv_batch_stride=0, causal=False, num_threads=0):
+    """Split partial over top-k range [k_begin, k_end): fp32 O [B*s_q,H,512], LSE [B*s_q,H]."""
+    q, kv, fmt, indices, seq_lens, block_table = _prep(q, kv, indices, seq_lens, block_table)
+    B, s_q, H, _ = q.shape
+    out = np.zeros((B, s_q, H, D_VO), np.uint16)
+    po = np.zeros((B * s_q, H, D_VO), np.float32)
+    pl = np.zeros((B * s_q, H), np.float32)
+    a = _decode_args(q, kv, fmt, indices, seq_lens, block_table, block_size, kv_batch_stride,
+                     causal, sm_scale, out, None)
+    rc = lib().oracle_mla_decode_partial(ctypes.byref(a), k_begin, k_end, _p(po), _p(pl),
+                                         num_threads)
+    assert rc == 0
+    return po, pl
+
+
+def mla_combine(part_o: np.ndarray, part_lse: np.ndarray):
+    """[S, rows, H, 512] + [S, rows, H] -> (bf16 bits [rows, H, 512], lse [rows, H])."""
+    po = np.ascontiguousarray(part_o, dtype=np.float32)
+    pl = np.ascontiguousarray(part_lse, dtype=np.float32)
+    S, rows, H, _ = po.shape
+    out = np.zeros((rows, H, D_VO), np.uint16)
+    lse = np.zeros((rows, H), np.float32)
+    lib().oracle_mla_combine(_p(po), _p(pl), S, rows, H, _p(out), _p(lse))
+    return out, lse
+
+
+def mla_prefill(q, kv, indices, sm_scale, *, causal=False, causal_offset=0, num_threads=0):
+    """Host oracle of dsa_mla_prefill: q uint16 [N,H,576], kv uint16 [rows,576] or uint8
+    [rows,656], indices int32 [N, topk]."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    kv = np.ascontiguousarray(kv)
+    fmt = KV_BF16 if kv.dtype == np.uint16 else KV_FP8_656
+    kv = kv.reshape(-1, D_QK if fmt == KV_BF16 else 656)
+    indices = np.ascontiguousarray(indices, dtype=np.int32)
+    N, H, _ = q.shape
+    out = np.zeros((N, H, D_VO), np.uint16)
+    lse = np.zeros((N, H), np.float32)
+    a = PrefillArgs()
+    a.q = _p(q)
+    a.q_stride_n, a.q_stride_h = H * D_QK, D_QK
+    a.kv = _p(kv)
+    a.kv_rows = kv.shape[0]
+    a.kv_format = fmt
+    a.indices = _p(indices)
+    a.idx_stride_n = indices.shape[1]
+    a.out = _p(out)
+    a.o_stride_n, a.o_stride_h = H * D_VO, D_VO
+    a.lse = _p(lse)
+    a.N, a.H, a.topk = N, H, indices.shape[1]
+    a.causal = 1 if causal else 0
+    a.causal_offset = causal_offset
+    a.sm_scale = float(sm_scale)
+    rc = lib().oracle_mla_prefill(ctypes.byref(a), num_threads)
+    assert rc == 0
+    return out, lse
+
+
+def num_threads(requested: int = 0) -> int:
+    return lib().oracle_num_threads(requested)
+
+
+# ------------------------------------------------------------- generators
+
+def normal_bf16(rng: np.random.Generator, shape) -> np.ndarray:
+    """~N(0,1) rounded to bf16 (bit patterns)."""
+    return bf16_bits(rng.standard_normal(shape, dtype=np.float32))
+
+
+def distinct_indices(rng: np.random.Generator, high: int, k: int) -> np.ndarray:
+    """k distinct positions drawn uniformly from [0, high), scattered order (k <= high)."""
+    return rng.choice(high, size=k, replace=False).astype(np.int32)
