@@ -211,9 +211,11 @@ def cpu_baseline_decode(d, fmt_fp8, sample_queries, unit_scale):
     oracle.mla_decode(q, kv, idx, sl, SM_SCALE, num_threads=nt)
     dt = time.perf_counter() - t0
     per_query = dt / len(picks)
+    scale = unit_scale / len(picks)
+    how = "the whole step" if len(picks) == unit_scale else f"scaled x{scale:.1f} to one step"
     return dict(value=per_query * unit_scale * 1e6, unit="us/step", cores=nt, kind="port",
                 sample=f"{len(picks)} of {B * s_q} query tokens (all 128 heads, full top-k), "
-                       f"{dt:.2f} s measured, scaled x{unit_scale / len(picks):.1f} to one step")
+                       f"{dt:.2f} s measured, {how}")
 
 
 def cpu_baseline_prefill(p, sample_queries, total_pairs):
@@ -221,7 +223,7 @@ def cpu_baseline_prefill(p, sample_queries, total_pairs):
     import torch
     import oracle
     N = p["q"].shape[0]
-    sel = torch.linspace(N // 2, N - 1, sample_queries).long()
+    sel = torch.linspace(0, N - 1, sample_queries).long()
     q = p["q"][sel].cpu().view(torch.int16).numpy().view(np.uint16)
     kv = p["kv"].cpu().view(torch.int16).numpy().view(np.uint16)
     idx = p["idx"][sel].cpu().numpy()
@@ -243,12 +245,19 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="c3", choices=[k for k in CONFIGS if k != "c5"])
+    ap.add_argument("--config", default="c3", choices=list(CONFIGS),
+                    help="decode workload of the JSON line (c5 only with --kernel-only)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-sample", type=int, default=4)
+    ap.add_argument("--cpu-sample", type=int, default=256,
+                    help="query tokens of the decode step the CPU oracle runs (256 = all of c3)")
+    ap.add_argument("--cpu-prefill-sample", type=int, default=2048,
+                    help="prefill queries (evenly spaced over [0, N)) the CPU oracle runs")
     ap.add_argument("--kernel-only", action="store_true",
-                    help="only run the timed decode steps (for profiler runs)")
+                    help="only run the timed steps of --config (for profiler runs)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="instead: run --steps plain device copies of MIB MiB (the reference "
+                         "kernel that scales rocprof FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -260,6 +269,27 @@ def main():
     load_library()
     dev = torch.device("cuda:0")
     cfg = CONFIGS[args.config]
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy << 20
+        src = torch.randint(0, 255, (n,), dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        ms = time_steps(lambda: dst.copy_(src), args.steps, args.warmup)
+        print(json.dumps({"copy_bytes": n, "ms_per_copy": ms,
+                          "GBps_read_plus_write": 2 * n / (ms * 1e-3) / 1e9}))
+        return
+    if cfg["kind"] == "prefill":
+        if not args.kernel_only:
+            ap.error("--config c5 is reported inside the default JSON line; use it with --kernel-only")
+        from opfoundry_amd import dsa
+        log("building c5 prefill inputs")
+        p = make_prefill(cfg, dev)
+        pout = torch.empty((p["q"].shape[0], H, D_VO), dtype=torch.bfloat16, device=dev)
+        plse = torch.empty((p["q"].shape[0], H), dtype=torch.float32, device=dev)
+        ms = time_steps(lambda: dsa.mla_prefill(p["q"], p["kv"], p["idx"], SM_SCALE, pout, plse),
+                        args.steps, args.warmup)
+        print(json.dumps({"config": args.config, "ms_per_step": ms}))
+        return
 
     log(f"building {args.config} inputs")
     d = make_decode(cfg, dev)
@@ -339,7 +369,7 @@ def main():
                                        "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                        "frac": round(pfl / (pms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}}
         if not args.no_cpu:
-            res["prefill"]["cpu_baseline"] = cpu_baseline_prefill(p, 4, pV)
+            res["prefill"]["cpu_baseline"] = cpu_baseline_prefill(p, args.cpu_prefill_sample, pV)
     print(json.dumps(res))
 
 

@@ -669,7 +669,7 @@ int ilog2(int v) { int s = 0; while ((1 << s) < v) ++s; return s; }
 int auto_splits(int64_t queries, int topk) {
     int ns = 1;
     const int min_split = (topk + MAX_CHUNK - 1) / MAX_CHUNK;
-    if (queries < 256) {
+    if (queries > 0 && queries < 256) {
         const int64_t want = (256 + queries - 1) / queries;
         const int64_t by_len = (topk + 255) / 256;  // keep >= 8 tiles per split
         ns = (int)std::min<int64_t>(want, std::max<int64_t>(1, by_len));
