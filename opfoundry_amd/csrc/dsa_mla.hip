@@ -1,24 +1,26 @@
 // dsa_mla.hip - gfx950 (MI355X) sparse MLA decode / prefill kernels and the
 // C ABI declared in include/dsa_mla.h.
 //
-// One workgroup handles one (query token, top-k split): 4 waves x 32 heads =
-// 128 heads, so every gathered latent row is read from HBM once and used by
-// all heads.  Per tile of 32 rows:
-//   gather   rows -> LDS ring with 16-byte LDS-DMA loads (global_load_lds);
-//            fp8 rows land raw and are dequantised cooperatively into the
-//            bf16 tile (e4m3 -> fp32 exact, times the per-128 scale, -> bf16)
-//   QK^T     S^T[32 rows x 32 heads] = K Q^T with 32x32x16 bf16 MFMA, Q held
-//            in registers for the whole workgroup lifetime
-//   softmax  exp2-domain softmax numerators against a fixed per-head
-//            reference max (no accumulator rescale in the loop); the
-//            per-head max is a lane-local max plus one cross-half exchange
-//   PV       O^T[512 x 32 heads] += V^T P^T, V^T read with ds_read_b64_tr_b16
-//            straight from the row-major tile, P^T taken from the S^T
-//            accumulator registers without any shuffle
-// The decode kernel design follows the reference's one-workgroup-per-work-item
-// structure (opus_attn/dsa_v32/gfx950/mla_decode_a16w16_32mxt_32nx1_template.hpp:
-// 916-1132) but is written from scratch for stock hipcc: no OPUS, no pinned
-// registers, 32x32 MFMA tiles, compacted index lists and a top-k index form.
+// Forward kernel: one workgroup per (query token, top-k split).  4 waves x 32
+// heads = 128 heads, so every gathered latent row is read from HBM once and
+// used by all heads.  The top-k list is first resolved to physical cache rows
+// and compacted (invalid entries dropped), then processed in tiles of 32 rows:
+//   gather   16-byte LDS-DMA loads (global_load_lds_dwordx4) of whole rows,
+//            issued 2 (bf16) / 3 (fp8) tiles ahead of use
+//   dequant  fp8 rows only: cooperative e4m3 -> fp16 conversion of the next
+//            tile (v_cvt_scalef32_pk_f16_fp8 applies the power-of-two part of
+//            the per-128 scale, v_pk_mul_f16 its mantissa), overlapped with the
+//            QK^T MFMAs of the current tile
+//   QK^T     S^T[32 rows x 32 heads] with 32x32x16 MFMAs (bf16, or fp16 for the
+//            fp8 cache), Q held in registers, two accumulator chains
+//   softmax  exp2 of the scores against a fixed per-head reference (the first
+//            tile's maximum): the O accumulators are never rescaled in the loop
+//   PV       O^T[512 x 32 heads] += V^T P^T, V^T read with ds_read_b64_tr_b16,
+//            P^T taken straight from the score registers
+// The structure follows the reference's one-workgroup-per-work-item decode
+// (opus_attn/dsa_v32/gfx950/mla_decode_a16w16_32mxt_32nx1_template.hpp:916-1132)
+// but is written from scratch for stock hipcc: no OPUS, no pinned registers,
+// a top-k index form, compacted index lists and an fp16 dequant path.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -38,54 +40,118 @@ constexpr int NWAVE = 4;
 constexpr int NTHR = NWAVE * 64;
 constexpr int TILE = 32;                   // latent rows per tile
 constexpr int MAX_CHUNK = 2048;            // top-k entries one workgroup can take
-constexpr int ROWB = D_QK * 2;             // bf16 cache row bytes (1152)
-// bf16 tile in LDS: NoPE rows at a 1040-byte stride (65 16-byte chunks, so the
-// 32 rows a K fragment touches fall in distinct bank groups), then the RoPE
-// block, 32 rows x 128 B with the chunks of row r XOR-swizzled by row_swz(r).
-constexpr int NOPE_STRIDE = 2 * D_NOPE + 16;            // 1040
-constexpr int ROPE_BASE = TILE * NOPE_STRIDE;          // 33280
-constexpr int ROPE_STRIDE = 2 * D_ROPE;                // 128
-constexpr int SLOT_BF16 = ROPE_BASE + TILE * ROPE_STRIDE;  // 37376
-constexpr int LD_BF16_PER_WAVE = TILE / NWAVE + 1;     // 8 NoPE rows + 1 RoPE block (9)
-constexpr int FP8_CH = DSA_MLA_FP8_ROW_BYTES / 16;  // 16-byte chunks per fp8 row (41)
-constexpr int LD_FP8_PER_WAVE = 6;                   // >= ceil(32*41/64/4), uniform per wave
-constexpr int SLOT_FP8 = LD_FP8_PER_WAVE * NWAVE * 1024;  // raw fp8 tile incl. pad (24576 B)
-constexpr int NS_BF16 = 3;                 // bf16-path ring depth
-constexpr int NS_RAW = 3;                  // fp8-path raw ring depth (+1 bf16 tile)
-constexpr int QK_REG = 28;                 // k-steps whose Q fragments live in registers (dims 0..447)
-constexpr int QL_DIMS = D_QK - 16 * QK_REG; // Q dims kept in LDS instead (448..575: 128)
-constexpr int QR_STRIDE = 2 * QL_DIMS + 16; // LDS bytes per head of that Q block (272)
+constexpr int KS_NOPE = D_NOPE / 16;       // 16-deep k-steps over the NoPE dims (32)
+constexpr int KS_ALL = D_QK / 16;          // all k-steps (36)
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float LN2 = 0.69314718055994531f;
-constexpr float RESTART_TAU = 64.0f;       // max growth of p over the reference max (log2 units)
+
+constexpr int BF16_ROW = DSA_MLA_BF16_ROW_BYTES;   // 1152
+constexpr int FP8_ROW = DSA_MLA_FP8_ROW_BYTES;     // 656
+
+// Tile buffer: 32 rows of 16-bit latent values (bf16, or fp16 after dequant).
+//   NoPE: row r at r * NOPE_STRIDE (1024 data bytes + 64 pad); its 16-byte
+//         chunk c sits at chunk position c ^ nope_sw(r).  The pad shifts every
+//         row by 4 bank groups, the XOR separates rows 4 apart, so both the K
+//         fragment reads (one chunk of 16 rows) and the transposed V reads
+//         (4 chunks of 4 rows) hit 16 distinct 16-byte bank groups.
+//   RoPE: row r at ROPE_OFF + 128 r, chunk c (0..7) at position c ^ rope_sw(r).
+constexpr int NOPE_STRIDE = 1088;
+constexpr int ROPE_OFF = TILE * NOPE_STRIDE;         // 34816
+constexpr int TILE_BYTES = ROPE_OFF + TILE * 128;    // 38912
+constexpr int RAW_BYTES = TILE * FP8_ROW;            // raw fp8 tile, rows back to back (20992)
+constexpr int FP8_CHUNKS = RAW_BYTES / 16;           // 16-byte chunks of a raw tile (1312)
+constexpr int FP8_LOADS = (FP8_CHUNKS + 63) / 64;    // wave-wide loads per raw tile (21)
+constexpr int FP8_LPW = (FP8_LOADS + NWAVE - 1) / NWAVE;  // loads of wave 0 (6); the others 5
+constexpr int BF16_LPW = TILE / NWAVE + 1;           // 8 NoPE rows + one 8-row RoPE block
+constexpr int FP8_SCALE_OFF = D_NOPE;                // 4 fp32 scales
+constexpr int FP8_ROPE_OFF = D_NOPE + 16;            // 64 bf16 RoPE values
+
+__device__ __forceinline__ int nope_sw(int r) { return (r >> 2) & 3; }
+__device__ __forceinline__ int rope_sw(int r) { return (r >> 1) & 7; }
+
+// LDS layout per cache format: tile buffers 0 and 1, then a ring region
+// (bf16: the third tile buffer; fp8: three raw slots), then the row list.
+template <int FMT>
+struct Lay {
+    static constexpr bool FP8 = FMT == DSA_KV_FP8_656;
+    static constexpr int RING_BYTES = FP8 ? 3 * RAW_BYTES : TILE_BYTES;
+    static constexpr int LPW = FP8 ? FP8_LPW : BF16_LPW;  // max DMA loads per wave per tile
+    // p = exp2(s - m_ref) may grow to 2^TAU over the reference before a
+    // restart: fp16 P (fp8 cache) is finite below 2^16, bf16 P below 2^128.
+    static constexpr float TAU = FP8 ? 15.0f : 100.0f;
+};
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 #define LDS_AS __attribute__((address_space(3)))
-#define GLB_AS __attribute__((address_space(1)))
 
 // 32-bit LDS addresses: every LDS access in the kernels goes through these
 // (a generic pointer would cost a 64-bit VGPR pair per address).
 typedef LDS_AS unsigned char* lds_ptr;
 typedef const LDS_AS unsigned char* lds_cptr;
 
-// 1152 zero bytes: invalid tile slots gather this row, so masked slots always
-// hold finite K and V = 0 (a poisoned cache row can never leak in as NaN * 0).
-__device__ __attribute__((aligned(16))) unsigned char g_zero_row[ROWB];
+template <class V>
+__device__ __forceinline__ V lds_ld(lds_cptr p) {
+    return *reinterpret_cast<const LDS_AS V*>(p);
+}
 
-// Swizzle of the 8 RoPE chunks of row r: chunk c lives at position c ^ x(r).
-// x is a bijection on every 8 consecutive rows and on the even / odd rows of
-// every 16, so 32 rows reading the same chunk spread over all bank groups of
-// a 32- or 64-bank LDS even though the RoPE rows are only 128 B apart.
-__device__ __forceinline__ int row_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+template <class V>
+__device__ __forceinline__ void lds_st(lds_ptr p, V v) {
+    *reinterpret_cast<LDS_AS V*>(p) = v;
+}
+
+__device__ __forceinline__ s16x4 lds_read_tr16(lds_cptr p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS s16x4*)(p));
+}
+
+// s_waitcnt vmcnt(N) with expcnt / lgkmcnt left at their maxima (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 0xF) | ((N >> 4) << 14));
+}
+
+// Keep an MFMA accumulator tile in AGPRs (an empty asm with an AGPR operand):
+// the O accumulators live there for the whole kernel.
+__device__ __forceinline__ void pin_acc(f32x16& v) { asm("" : "+a"(v)); }
+// Opaque copy: stops the compiler from hoisting per-lane address math out of
+// the tile loop (which would pin dozens of loop-invariant VGPRs).
+__device__ __forceinline__ int opaque(int v) {
+    asm("" : "+v"(v));
+    return v;
+}
+
+// 16-byte LDS-DMA load: lane l's 16 bytes from gsrc land at lds_wave_base +
+// 16*l.  Issued through inline asm so the compiler neither waits on it at the
+// next LDS read nor folds it into its own vmcnt accounting: the tile loop
+// tracks these loads with explicit s_waitcnt vmcnt(N), and no other vector
+// memory load is issued inside the loop.
+__device__ __forceinline__ void lds_dma16(const void* gsrc, lds_ptr lds_wave_base) {
+    const unsigned m0v = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_wave_base);
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off"
+        :
+        : "s"(m0v), "v"(gsrc)
+        : "memory", "m0");
+}
+
+// Workgroup barrier for the tile loop: LDS accesses of this wave complete,
+// then s_barrier.  Unlike __syncthreads() it does not drain vector memory, so
+// the LDS-DMA gathers of later tiles stay in flight across it.
+__device__ __forceinline__ void tile_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 struct FwdParams {
     const __bf16* q;
@@ -113,63 +179,6 @@ struct FwdParams {
     float scale_log2;            // sm_scale * log2(e)
 };
 
-__device__ __forceinline__ void wait_vmcnt_le(int n) {
-    // s_waitcnt vmcnt(n), expcnt/lgkmcnt left at their maxima (gfx9 encoding).
-    switch (n) {
-    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
-    case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
-    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
-    case 18: __builtin_amdgcn_s_waitcnt(0x4F72); break;
-    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-    }
-}
-
-// Keep an MFMA accumulator tile in AGPRs (an empty asm with an AGPR operand):
-// the O accumulators stay there for the whole kernel and only the rare
-// rescale moves them through VGPRs.
-__device__ __forceinline__ void pin_acc(f32x16& v) { asm volatile("" : "+a"(v)); }
-// Keep a tile the VALU reads next (the score accumulator) in VGPRs.
-__device__ __forceinline__ void pin_vgpr(f32x16& v) { asm volatile("" : "+v"(v)); }
-
-// Opaque copy: stops the compiler from hoisting per-lane address math out of
-// the tile loop (which would pin dozens of loop-invariant VGPRs).
-__device__ __forceinline__ int opaque(int v) {
-    asm volatile("" : "+v"(v));
-    return v;
-}
-
-// 16-byte LDS-DMA load: lane l's 16 bytes from gsrc land at lds_wave_base +
-// 16*l.  Issued through inline asm so the compiler neither waits on it at the
-// next LDS read nor folds it into its own vmcnt accounting: the tile loop
-// tracks these loads itself with explicit s_waitcnt vmcnt(N) (wait_vmcnt_le),
-// and no other vector-memory load is issued inside the loop.
-__device__ __forceinline__ void lds_dma16(const void* gsrc, lds_ptr lds_wave_base) {
-    const unsigned m0v = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_wave_base);
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, off"
-        :
-        : "s"(m0v), "v"(gsrc)
-        : "memory", "m0");
-}
-
-// Workgroup barrier for the tile loop: LDS writes of this wave complete, then
-// s_barrier.  Unlike __syncthreads() it does not drain vector memory, so the
-// LDS-DMA gathers of later tiles stay in flight across it.
-__device__ __forceinline__ void tile_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-__device__ __forceinline__ bf16x8 lds_read_b128(lds_cptr p) {
-    return *reinterpret_cast<const LDS_AS bf16x8*>(p);
-}
-
-__device__ __forceinline__ s16x4 lds_read_tr16(lds_cptr p) {
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS_AS s16x4*)(p));
-}
-
 // Physical cache row of logical position j of query (b, t); -1 if invalid.
 __device__ __forceinline__ int64_t resolve_row(const FwdParams& p, int b, int64_t jmax, int32_t j) {
     if (j < 0 || (int64_t)j >= jmax) return -1;
@@ -186,6 +195,28 @@ __device__ __forceinline__ int64_t resolve_row(const FwdParams& p, int b, int64_
     return row;
 }
 
+// One piece of the fp8 dequant in flight: codes + scale, or 16 RoPE bytes.
+struct DeqPiece {
+    u32x4 v;
+};
+constexpr int DEQ_PIECES = TILE / NWAVE + 1;
+
+__device__ __forceinline__ f32x16 mfma_bf16(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma_f16(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// bf16 pair -> fp16 pair.  Exact for |x| in [2^-14, 65504]; smaller values go
+// to fp16 subnormals (truncated, absolute error < 2^-24).
+__device__ __forceinline__ unsigned bf16x2_to_f16x2(unsigned w) {
+    const float lo = __uint_as_float(w << 16), hi = __uint_as_float(w & 0xFFFF0000u);
+    return __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+}
+
 // ---------------------------------------------------------------------------
 // Fused sparse-MLA forward: one workgroup per (query token, split).
 // grid = (B, s_q, num_splits), block = 256.
@@ -193,36 +224,50 @@ __device__ __forceinline__ int64_t resolve_row(const FwdParams& p, int b, int64_
 template <int FMT>
 __global__ void __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(1, 1)))
 dsa_mla_fwd_kernel(const FwdParams p) {
-    constexpr int NS = FMT == DSA_KV_BF16 ? NS_BF16 : NS_RAW;
-    constexpr int RAW_SLOT = FMT == DSA_KV_BF16 ? SLOT_BF16 : SLOT_FP8;
-    __shared__ __attribute__((aligned(1024))) unsigned char s_raw[NS * RAW_SLOT];
-    // fp8 only: the dequantised bf16 tile.  One buffer suffices: the tile
-    // barrier at the top of each iteration orders compute(it-1) before
-    // dequant(it).
-    __shared__ __attribute__((aligned(1024))) unsigned char s_bf[FMT == DSA_KV_BF16 ? 16 : SLOT_BF16];
-    // Tail of Q (dims 448..575), [128 heads][128] bf16 with a 272-byte head
-    // stride (the 16-byte pad spreads 16 consecutive heads over distinct bank
-    // groups).  Holding it here instead of in registers leaves the tile loop
-    // enough VGPRs to run without spills.
-    __shared__ __attribute__((aligned(16))) unsigned char s_qr[HEADS * QR_STRIDE];
-    __shared__ int32_t s_rows[MAX_CHUNK];
-    __shared__ int s_wsum[NWAVE];
-    __shared__ int s_restart;
-    const lds_ptr L_raw = (lds_ptr)s_raw;
-    const lds_ptr L_bf = (lds_ptr)s_bf;
-    const lds_ptr L_qr = (lds_ptr)s_qr;
+    using L = Lay<FMT>;
+    constexpr bool FP8 = L::FP8;
+    // Separate LDS objects for the tile buffers: the compiler can then prove
+    // that the dequant stores into one buffer never alias the K / V reads of
+    // the other, and interleave them with the MFMAs.
+    __shared__ __attribute__((aligned(1024))) unsigned char s_tile0[TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) unsigned char s_tile1[TILE_BYTES];
+    // bf16: the third ring buffer; fp8: the three raw slots
+    __shared__ __attribute__((aligned(1024))) unsigned char s_ring[L::RING_BYTES];
+    __shared__ int32_t s_rows_arr[MAX_CHUNK];
+    // P exchange: [u][source wave][hi][head lane] x 16 bytes (8 P values), so
+    // a B-operand fragment of the PV MFMA is one contiguous 16-byte read
+    __shared__ __attribute__((aligned(16))) unsigned char s_p[2 * NWAVE * 64 * 16];
+    __shared__ int s_misc_arr[16];            // [0..3] wave sums, [4] restart flag
+    const lds_ptr T0 = (lds_ptr)s_tile0;
+    const lds_ptr T1 = (lds_ptr)s_tile1;
+    const lds_ptr RING = (lds_ptr)s_ring;
+    const lds_ptr PX = (lds_ptr)s_p;
+    LDS_AS int32_t* const s_rows = (LDS_AS int32_t*)s_rows_arr;
+    LDS_AS int* const s_misc = (LDS_AS int*)s_misc_arr;
 
     const int b = blockIdx.x, t = blockIdx.y, split = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) s_restart = 0;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hi = lane >> 5, r32 = lane & 31;
+    const int head = wave * 32 + r32;
+    if (tid == 0) s_misc[4] = 0;
+
+    // ---- 0. Q fragments (B operand of S^T = K Q^T): lane -> head r32, k-chunk hi ----
+    // Issued first so their latency overlaps the index resolution below.
+    u32x4 qf[KS_ALL];
+    {
+        const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head * p.q_sh + 8 * hi;
+#pragma unroll
+        for (int ks = 0; ks < KS_ALL; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * ks);
+    }
 
     // ---- 1. resolve this split's index chunk into a compacted row list ----
     const int k0 = split * p.chunk;
     const int k1 = min(k0 + p.chunk, p.topk);
-    int64_t L = p.seq_lens ? (int64_t)p.seq_lens[b] : p.seq_len_default;
-    int64_t jmax = L;
-    if (p.causal == 1) jmax = min(L, L - p.s_q + t + 1);
-    else if (p.causal == 2) jmax = min(L, (int64_t)b + p.causal_offset + 1);
+    const int64_t Lq = p.seq_lens ? (int64_t)p.seq_lens[b] : p.seq_len_default;
+    int64_t jmax = Lq;
+    if (p.causal == 1) jmax = min(Lq, Lq - p.s_q + t + 1);
+    else if (p.causal == 2) jmax = min(Lq, (int64_t)b + p.causal_offset + 1);
     const int32_t* idx = p.indices + (int64_t)b * p.idx_sb + (int64_t)t * p.idx_st;
 
     constexpr int PER_T = MAX_CHUNK / NTHR;  // 8 entries per thread
@@ -241,19 +286,18 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             cnt += rows_local[e] >= 0 ? 1 : 0;
         }
     }
-    // block-wide exclusive scan of cnt
     int incl = cnt;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
         const int v = __shfl_up(incl, off, 64);
         if (lane >= off) incl += v;
     }
-    if (lane == 63) s_wsum[wave] = incl;
+    if (lane == 63) s_misc[wave] = incl;
     __syncthreads();
     int wbase = 0, n_valid = 0;
 #pragma unroll
     for (int w = 0; w < NWAVE; ++w) {
-        const int s = s_wsum[w];
+        const int s = s_misc[w];
         wbase += w < wave ? s : 0;
         n_valid += s;
     }
@@ -265,295 +309,440 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     }
     __syncthreads();
     const int ntiles = (n_valid + TILE - 1) / TILE;
-
-    // ---- 2. Q fragments: B operand of S^T = K Q^T, lane -> head lane%32 ----
-    const int h32 = lane & 31, hi = lane >> 5;
-    const int head = wave * 32 + h32;
-    bf16x8 qf[QK_REG];
-    {
-        const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head * p.q_sh + 8 * hi;
-#pragma unroll
-        for (int ks = 0; ks < QK_REG; ++ks)
-            qf[ks] = *reinterpret_cast<const bf16x8*>(qp + 16 * ks);
-        // Q tail -> LDS: 128 heads x 16 chunks of 16 B, 8 per thread
-        const __bf16* qb = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + 16 * QK_REG;
-#pragma unroll
-        for (int i = 0; i < (HEADS * QL_DIMS / 8) / NTHR; ++i) {
-            const int u = tid + NTHR * i;
-            const int hh = u / (QL_DIMS / 8), c = u % (QL_DIMS / 8);
-            *reinterpret_cast<LDS_AS u32x4*>(L_qr + hh * QR_STRIDE + 16 * c) =
-                *reinterpret_cast<const u32x4*>(qb + (int64_t)hh * p.q_sh + 8 * c);
-        }
-    }
-    // Q fragments complete before the tile loop: inside the loop the only
-    // vector-memory loads are the LDS-DMA gathers counted by wait_vmcnt_le.
-    __builtin_amdgcn_s_waitcnt(0x0F70);
+    // Pad the last tile with copies of the first valid row: every gathered
+    // row is finite cache data, and the softmax masks the padding rows.
+    if (tid < TILE && n_valid > 0 && n_valid + tid < ntiles * TILE) s_rows[n_valid + tid] = s_rows[0];
     __syncthreads();
-    lds_cptr qr_lane = L_qr + head * QR_STRIDE + 16 * hi;
 
-    // ---- gather issue: tile `it` into ring slot `slot` ----
-    auto issue_tile = [&](int it, int slot) {
+    // bf16 ring slot -> tile buffer
+    auto slot_buf = [&](int s) -> lds_ptr { return s == 0 ? T0 : (s == 1 ? T1 : RING); };
+
+    // ---- 2. gather: rows of tile `ti` -> ring slot `slot` ----
+    // Every load is a full wave-wide LDS-DMA load of 1 KB: the number of
+    // loads a CU can keep in flight is limited, so each one carries as much
+    // as it can.  bf16: wave w loads NoPE rows 8w..8w+7 (one row per load)
+    // plus one load covering the 8 RoPE blocks; fp8: the raw tile's 1312
+    // 16-byte chunks (rows back to back) are 21 loads, wave w taking loads
+    // w, w+4, ... (6 for wave 0, 5 for the others).  The row ids of the next
+    // tile to issue are read from the row list a step ahead (GatherRows).
+    struct GatherRows {
+        int32_t r[FP8 ? FP8_LPW : TILE / NWAVE];  // bf16: this wave's rows (uniform); fp8: per lane
+        int32_t rope;                             // bf16: row of this lane's RoPE chunk
+    };
+    const int my_loads = FP8 ? (wave < FP8_LOADS - NWAVE * (FP8_LPW - 1) ? FP8_LPW : FP8_LPW - 1) : L::LPW;
+    auto load_rows = [&](int ti) -> GatherRows {
+        const LDS_AS int32_t* rows = s_rows + ti * TILE;
         const int ln = opaque(lane);
-        if constexpr (FMT == DSA_KV_BF16) {
-            lds_ptr slot_base = L_raw + slot * RAW_SLOT;
-            // NoPE: one wave instruction per row, lane = 16-byte chunk
+        GatherRows g;
+        if constexpr (!FP8) {
 #pragma unroll
-            for (int i = 0; i < TILE / NWAVE; ++i) {
-                const int r = (TILE / NWAVE) * wave + i;
-                const int row = it * TILE + r;
-                const unsigned char* src = row < n_valid ? p.kv + (int64_t)s_rows[row] * ROWB : g_zero_row;
-                lds_dma16(src + 16 * ln, slot_base + r * NOPE_STRIDE);
-            }
-            // RoPE: rows 8w..8w+7, lane -> (row 8w + lane/8, LDS position lane%8)
-            {
-                const int r = (TILE / NWAVE) * wave + (ln >> 3);
-                const int row = it * TILE + r;
-                const int c = (ln & 7) ^ row_swz(r);  // global RoPE chunk stored at position lane%8
-                const unsigned char* src = row < n_valid ? p.kv + (int64_t)s_rows[row] * ROWB : g_zero_row;
-                lds_dma16(src + 2 * D_NOPE + 16 * c, slot_base + ROPE_BASE + (TILE / NWAVE) * wave * ROPE_STRIDE);
-            }
+            for (int i = 0; i < TILE / NWAVE; ++i) g.r[i] = __builtin_amdgcn_readfirstlane(rows[8 * wave + i]);
+            g.rope = rows[8 * wave + (ln >> 3)];
         } else {
 #pragma unroll
-            for (int i = 0; i < LD_FP8_PER_WAVE; ++i) {
+            for (int i = 0; i < FP8_LPW; ++i) {
+                const int c16 = 64 * (wave + NWAVE * i) + ln;      // linear chunk of the raw tile
+                g.r[i] = rows[min((c16 * 1599) >> 16, TILE - 1)];  // c16 / 41
+            }
+            g.rope = 0;
+        }
+        return g;
+    };
+    // i-th load of this wave for a tile
+    auto issue_one = [&](const GatherRows& g, int slot, int i) {
+        const int ln = opaque(lane);
+        if constexpr (!FP8) {
+            const lds_ptr tb = slot_buf(slot);
+            if (i < 8) {
+                const int r = 8 * wave + i;
+                const unsigned char* src = p.kv + (int64_t)g.r[i] * BF16_ROW + 16 * (ln ^ nope_sw(r));
+                lds_dma16(src, tb + r * NOPE_STRIDE);
+            } else {
+                const int r = 8 * wave + (ln >> 3);
+                const unsigned char* src =
+                    p.kv + (int64_t)g.rope * BF16_ROW + 2 * D_NOPE + 16 * ((ln & 7) ^ rope_sw(r));
+                lds_dma16(src, tb + ROPE_OFF + 8 * wave * 128);
+            }
+        } else {
+            if (i < my_loads) {
                 const int k = wave + NWAVE * i;
-                const int pch = 64 * k + ln;
-                const int r = pch / FP8_CH, c = pch - r * FP8_CH;
-                const int slot_row = it * TILE + r;
-                const unsigned char* src = (r < TILE && slot_row < n_valid)
-                    ? p.kv + (int64_t)s_rows[slot_row] * DSA_MLA_FP8_ROW_BYTES + 16 * c
-                    : g_zero_row;
-                lds_dma16(src, L_raw + slot * RAW_SLOT + 1024 * k);
+                const int c16 = 64 * k + ln;
+                const int c = c16 - 41 * ((c16 * 1599) >> 16);
+                const unsigned char* src = p.kv + (int64_t)g.r[i] * FP8_ROW + 16 * c;
+                if (c16 < FP8_CHUNKS) lds_dma16(src, RING + slot * RAW_BYTES + 1024 * k);
             }
         }
     };
-
-    constexpr int LOADS_PER_TILE = FMT == DSA_KV_BF16 ? LD_BF16_PER_WAVE : LD_FP8_PER_WAVE;
-
-    // ---- fp8: dequantise raw slot -> bf16 tile (cooperative) ----
-    auto dequant_tile = [&](lds_cptr raw, lds_ptr dst) {
-        // NoPE: 32 rows x 32 groups of 16 codes = 1024 units, 4 per thread.
+    auto issue_rows = [&](const GatherRows& g, int slot) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int u = tid + NTHR * i;
-            const int r = u >> 5, q16 = u & 31;
-            lds_cptr rr = raw + r * DSA_MLA_FP8_ROW_BYTES;
-            const u32x4 codes = *reinterpret_cast<const LDS_AS u32x4*>(rr + 16 * q16);
-            const float sc = *reinterpret_cast<const LDS_AS float*>(rr + D_NOPE + 4 * (q16 >> 3));
-            u32x4 lo, hi2;
+        for (int i = 0; i < L::LPW; ++i) issue_one(g, slot, i);
+    };
+    // wait until this wave's loads of all but the newest `keep` tiles landed
+    auto wait_tiles = [&](int keep) {
+        if (keep <= 0) wait_vm<0>();
+        else if constexpr (FP8) {
+            if (keep == 1) { if (my_loads == FP8_LPW) wait_vm<FP8_LPW>(); else wait_vm<FP8_LPW - 1>(); }
+            else { if (my_loads == FP8_LPW) wait_vm<2 * FP8_LPW>(); else wait_vm<2 * (FP8_LPW - 1)>(); }
+        } else {
+            if (keep == 1) wait_vm<L::LPW>();
+            else wait_vm<2 * L::LPW>();
+        }
+    };
+
+    // ---- 3. fp8: dequantise a raw slot into a tile buffer (cooperative) ----
+    // Nine pieces per tile.  Pieces 0..7: wave w converts row w + 4j; lane l
+    // owns NoPE codes 8l..8l+7 (scale group l/16); fp16 = fp16(code * 2^e) *
+    // fp16(mantissa) where scale = mantissa * 2^e.  Piece 8: RoPE, copied as
+    // bf16 (one 16-byte chunk per thread).
+    auto deq_load = [&](lds_cptr rb, int j) -> DeqPiece {
+        const int ln = opaque(lane);
+        DeqPiece d;
+        if (j < TILE / NWAVE) {
+            const lds_cptr rr = rb + (wave + NWAVE * j) * FP8_ROW;
+            const u32x2 codes = lds_ld<u32x2>(rr + 8 * ln);
+            d.v[0] = codes[0];
+            d.v[1] = codes[1];
+            d.v[2] = __float_as_uint(lds_ld<float>(rr + FP8_SCALE_OFF + 4 * (ln >> 4)));
+            d.v[3] = 0;
+        } else {
+            const int t8 = opaque(tid);
+            d.v = lds_ld<u32x4>(rb + (t8 >> 3) * FP8_ROW + FP8_ROPE_OFF + 16 * (t8 & 7));
+        }
+        return d;
+    };
+    auto deq_store = [&](lds_ptr tb, int j, const DeqPiece& d) {
+        const int ln = opaque(lane);
+        if (j < TILE / NWAVE) {
+            const int r = wave + NWAVE * j;
+            const float sc = __uint_as_float(d.v[2]);
+            const _Float16 m16 = (_Float16)__uint_as_float((d.v[2] & 0x007FFFFFu) | 0x3F800000u);
+            const f16x2 mm = {m16, m16};
+            const f16x2 h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)d.v[0], sc, false) * mm;
+            const f16x2 h1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)d.v[0], sc, true) * mm;
+            const f16x2 h2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)d.v[1], sc, false) * mm;
+            const f16x2 h3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)d.v[1], sc, true) * mm;
+            const u32x4 out = {__builtin_bit_cast(unsigned, h0), __builtin_bit_cast(unsigned, h1),
+                               __builtin_bit_cast(unsigned, h2), __builtin_bit_cast(unsigned, h3)};
+            lds_st<u32x4>(tb + r * NOPE_STRIDE + 16 * (ln ^ nope_sw(r)), out);
+        } else {
+            const int t8 = opaque(tid);
+            const int r = t8 >> 3, c = t8 & 7;
+            lds_st<u32x4>(tb + ROPE_OFF + 128 * r + 16 * (c ^ rope_sw(r)), d.v);
+        }
+    };
+    auto dequant = [&](lds_cptr rb, lds_ptr tb) {
+#pragma unroll
+        for (int j = 0; j < DEQ_PIECES; ++j) deq_store(tb, j, deq_load(rb, j));
+    };
+
+    // ---- online softmax state (fixed reference max) ----
+    // p = exp2(s*c - m_ref) with m_ref fixed for the whole pass (the first
+    // tile's maximum per head), so the O accumulators are never rescaled in
+    // the loop.  If some p exceeds 2^TAU (a later score grew past the range of
+    // the P format) the restart flag is raised; the workgroup then reruns the
+    // tiles with m_ref raised by log2 of the largest p seen, an upper bound of
+    // the true maximum.
+    const float c_s = p.scale_log2;
+    // O^T accumulators of this wave: dims 128*wave + 32*m + (0..31) for the
+    // 32 heads 32*h + (0..31): o[4*m + h] (the PV step is split by output
+    // dims across the waves, so each gathered V value is read by one wave).
+    f32x16 o[D_VO / 32];
+    float m_ref = 0.0f, l_lane = 0.0f, e_max = 0.0f;
+    constexpr int NPRE = FP8 ? 3 : 2;       // tiles in flight before the loop
+    GatherRows gnext;
+#pragma unroll
+    for (int s = 0; s < NPRE; ++s)
+        if (s < ntiles) issue_rows(load_rows(s), s);
+    if (NPRE < ntiles) gnext = load_rows(NPRE);
+
+    if constexpr (FP8) {
+        // the NoPE part of Q is converted to fp16 for the fp16 MFMAs
+#pragma unroll
+        for (int ks = 0; ks < KS_NOPE; ++ks)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) qf[ks][w] = bf16x2_to_f16x2(qf[ks][w]);
+    }
+    // Q (and the first gathers) complete before the tile loop: inside the loop
+    // the only vector-memory loads are the LDS-DMA gathers counted explicitly.
+    wait_vm<0>();
+
+    // P values -> MFMA operand (bf16 for the bf16 cache, fp16 for fp8)
+    auto to_p = [&](const float* e) -> u32x4 {
+        u32x4 pb;
+        if constexpr (FP8) {
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)codes[w], false);
-                const f32x2 c2 = __builtin_amdgcn_cvt_pk_f32_fp8((int)codes[w], true);
-                const bf16x2 ba = __builtin_convertvector(a * sc, bf16x2);
-                const bf16x2 bc = __builtin_convertvector(c2 * sc, bf16x2);
-                const unsigned ua = __builtin_bit_cast(unsigned, ba);
-                const unsigned uc = __builtin_bit_cast(unsigned, bc);
-                if (w < 2) { lo[2 * w] = ua; lo[2 * w + 1] = uc; }
-                else { hi2[2 * (w - 2)] = ua; hi2[2 * (w - 2) + 1] = uc; }
+                const f16x2 h = {(_Float16)e[2 * w], (_Float16)e[2 * w + 1]};
+                pb[w] = __builtin_bit_cast(unsigned, h);
             }
-            lds_ptr drow = dst + r * NOPE_STRIDE + 32 * q16;  // bf16 chunks 2q16, 2q16+1
-            *reinterpret_cast<LDS_AS u32x4*>(drow) = lo;
-            *reinterpret_cast<LDS_AS u32x4*>(drow + 16) = hi2;
+        } else {
+            const f32x8 a = {e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]};
+            pb = __builtin_bit_cast(u32x4, __builtin_convertvector(a, bf16x8));
         }
-        // RoPE: 32 rows x 8 chunks of 8 bf16 = 256 units, 1 per thread.
-        {
-            const int r = tid >> 3, c = tid & 7;
-            const u32x4 v = *reinterpret_cast<const LDS_AS u32x4*>(
-                raw + r * DSA_MLA_FP8_ROW_BYTES + 528 + 16 * c);
-            *reinterpret_cast<LDS_AS u32x4*>(
-                dst + ROPE_BASE + r * ROPE_STRIDE + 16 * (c ^ row_swz(r))) = v;
-        }
+        return pb;
     };
 
-    // ---- online softmax with a fixed reference max ----
-    // p = exp2(s - m_ref) with m_ref fixed for the whole pass (the first tile's
-    // max per head), so the O accumulators are never rescaled inside the tile
-    // loop.  p may grow up to 2^RESTART_TAU (fp32 / bf16 have the range and
-    // the result is scale-invariant).  A tile whose max exceeds m_ref + TAU
-    // raises s_restart; after the pass the workgroup restarts from tile 0 with
-    // m_ref = the largest score seen, discarding the partial sums.  For inputs whose
-    // scores stay within 2^64 of the first tile's maximum this never happens.
-    f32x16 o[D_VO / 32];
-    float m_ref = -INFINITY, m_seen = -INFINITY, l_lane = 0.0f;
+    // ---- one tile: QK^T (+ gathers of a later tile), softmax, PV (+ dequant of the next tile) ----
+    // kt: buffer holding tile `it`; nxt: fp8 only, buffer receiving tile it+1.
+    bool first_tile = true;
+    auto step = [&](int it, lds_cptr kt, lds_ptr nxt) {
+        // per-lane offsets inside the tile buffer (recomputed per tile)
+        const int ln = opaque(lane);
+        const int lhi = ln >> 5, lr = ln & 31;
+        // K fragment of k-step ks (A operand of S^T = K Q^T): row lr, chunk 2ks+hi
+        const lds_cptr k_even = kt + lr * NOPE_STRIDE + 16 * (lhi ^ nope_sw(lr));
+        const lds_cptr k_odd = kt + lr * NOPE_STRIDE + 16 * ((2 + lhi) ^ nope_sw(lr));
+        const lds_cptr k_rope = kt + ROPE_OFF + 128 * lr;
+        const int rsw = rope_sw(lr);
 
-    for (;;) {
+        // ---- S^T = K Q^T (32 rows x 32 heads) ----
+        // Software pipeline pinned with scheduling barriers: the K fragment of
+        // k-step ks+KPF is read while MFMA ks runs; the gathers of tile
+        // it+NPRE are issued between the MFMAs (one load every 4 k-steps).
+        constexpr int KPF = 4;
+        auto k_addr = [&](int ks) -> lds_cptr {
+            return ks < KS_NOPE ? ((ks & 1) ? k_odd : k_even) + 64 * (ks >> 1)
+                                : k_rope + 16 * ((2 * (ks - KS_NOPE) + lhi) ^ rsw);
+        };
+        const bool do_issue = it + NPRE < ntiles;
+        const int issue_slot = FP8 ? it % 3 : (it + 2) % 3;
+        const GatherRows gcur = gnext;
+        __builtin_amdgcn_sched_barrier(0);
+        u32x4 kb[KPF];
+#pragma unroll
+        for (int i = 0; i < KPF; ++i) kb[i] = lds_ld<u32x4>(k_addr(i));
+        f32x16 sacc = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < KS_ALL; ++ks) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (FP8 && ks < KS_NOPE) sacc = mfma_f16(kb[ks % KPF], qf[ks], sacc);
+            else sacc = mfma_bf16(kb[ks % KPF], qf[ks], sacc);
+            if (ks + KPF < KS_ALL) kb[ks % KPF] = lds_ld<u32x4>(k_addr(ks + KPF));
+            if (FP8 && ks % 6 == 1 && ks / 6 < FP8_LPW && do_issue) issue_one(gcur, issue_slot, ks / 6);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // row ids of the tile issued in the next step
+        if (it + NPRE + 1 < ntiles) gnext = load_rows(it + NPRE + 1);
+
+        // ---- softmax numerators -> P (this wave's 32 heads) ----
+        // lane (hi, r32), reg r holds row 8*(r/4) + 4*hi + r%4 of head r32:
+        // regs 0..7 are rows 0..15 (PV k-step u = 0), regs 8..15 rows 16..31.
+        const int rows_left = n_valid - it * TILE;
+        if (first_tile) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = 8 * (r >> 2) + 4 * hi + (r & 3);
+                mx = fmaxf(mx, row < rows_left ? sacc[r] : -INFINITY);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            m_ref = mx * c_s;
+            first_tile = false;
+        }
+        if (rows_left < TILE) {
+            // last tile: the padding rows get no weight
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = 8 * (r >> 2) + 4 * hi + (r & 3);
+                sacc[r] = row < rows_left ? sacc[r] : -INFINITY;
+            }
+        }
+        if (ntiles == 1 && it == 0) {
+            // Single-tile list: fold the exact sum into the reference, so
+            // that p = exp2(s - m_ref) is already normalised when it is
+            // rounded - the order the reference uses
+            // (opus_attn/dsa_v32/common/host.cc:448-451); with few rows the
+            // outputs are large and a different rounding order would show.
+            float lt = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) lt += __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], c_s, -m_ref));
+            m_ref += __builtin_amdgcn_logf(lt + __shfl_xor(lt, 32, 64));
+        }
+        {
+            float e[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], c_s, -m_ref));
+            float lt = 0.0f, em = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                lt += e[r];
+                em = fmaxf(em, e[r]);
+            }
+            l_lane += lt;
+            e_max = fmaxf(e_max, em);
+            lds_st<u32x4>(PX + ((0 * NWAVE + wave) * 64 + ln) * 16, to_p(e));
+            lds_st<u32x4>(PX + ((1 * NWAVE + wave) * 64 + ln) * 16, to_p(e + 8));
+        }
+        tile_barrier();     // every wave's P is visible
+
+        // ---- O^T[128 dims of this wave x 128 heads] += V^T P^T ----
+        // Transposed V reads: 16-lane group g16 reads rows R..R+3 (lane
+        // 4rr+pp: row R+rr, dims d0+4pp..+3) with R = 16u + 4hi and R + 8.
+        // fp8: the dequant of the next tile runs between the MFMAs.
+        {
+            const int g16 = ln >> 4, i16 = ln & 15, rr = i16 >> 2, pp = i16 & 3;
+            const int vx = 2 * (g16 & 1) + (pp >> 1);
+            const lds_cptr v_a = kt + (4 * lhi + rr) * NOPE_STRIDE + 16 * (vx ^ lhi) + 8 * (pp & 1) + 256 * wave;
+            const lds_cptr v_b = kt + (4 * lhi + rr + 8) * NOPE_STRIDE + 16 * (vx ^ (lhi + 2)) + 8 * (pp & 1) + 256 * wave;
+            const lds_cptr draw = FP8 ? RING + ((it + 1) % 3) * RAW_BYTES : kt;
+            auto v_frag = [&](int u, int m) -> u32x4 {
+                const s16x4 va = lds_read_tr16(v_a + 16 * u * NOPE_STRIDE + 64 * m);
+                const s16x4 vb = lds_read_tr16(v_b + 16 * u * NOPE_STRIDE + 64 * m);
+                return __builtin_bit_cast(u32x4, __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7));
+            };
+            DeqPiece dq[2];
+            int step_i = 0;   // MFMA-group counter (8 groups of 4 MFMAs)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                u32x4 pbf[NWAVE];
+#pragma unroll
+                for (int h = 0; h < NWAVE; ++h) pbf[h] = lds_ld<u32x4>(PX + ((u * NWAVE + h) * 64 + ln) * 16);
+                u32x4 va_cur = v_frag(u, 0);
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    const u32x4 va_nxt = m + 1 < 4 ? v_frag(u, m + 1) : va_cur;
+#pragma unroll
+                    for (int h = 0; h < NWAVE; ++h) {
+                        o[4 * m + h] = FP8 ? mfma_f16(va_cur, pbf[h], o[4 * m + h]) : mfma_bf16(va_cur, pbf[h], o[4 * m + h]);
+                        pin_acc(o[4 * m + h]);
+                    }
+                    if constexpr (FP8) {
+                        // piece j: loads in MFMA group j, conversion + store in group j+1
+                        const int j = step_i;
+                        dq[j & 1] = deq_load(draw, j);
+                        if (j >= 1) deq_store(nxt, j - 1, dq[(j - 1) & 1]);
+                    } else if (do_issue) {
+                        // gathers of tile it+2: one load per MFMA group (two in the first)
+                        if (step_i == 0) issue_one(gcur, issue_slot, 8);
+                        issue_one(gcur, issue_slot, step_i);
+                    }
+                    va_cur = va_nxt;
+                    ++step_i;
+                }
+            }
+            if constexpr (FP8) {
+                // pieces 0..7 were loaded in the 8 MFMA groups, 0..6 stored
+                static_assert(DEQ_PIECES == 9, "dequant pieces vs MFMA groups");
+                __builtin_amdgcn_sched_barrier(0);
+                deq_store(nxt, 7, dq[1]);
+                deq_store(nxt, 8, deq_load(draw, 8));
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    for (int pass = 0;; ++pass) {
 #pragma unroll
         for (int mb = 0; mb < D_VO / 32; ++mb) {
             o[mb] = f32x16{};
             pin_acc(o[mb]);
         }
+        l_lane = 0.0f;
+        e_max = 0.0f;
+        first_tile = pass == 0;
+        if (pass > 0) {
 #pragma unroll
-        for (int s = 0; s < NS - 1; ++s)
-            if (s < ntiles) issue_tile(s, s);
-
-        for (int it = 0; it < ntiles; ++it) {
-            // tile `it` must have landed; newer tiles may stay in flight
-            if (it + NS - 2 < ntiles) wait_vmcnt_le(LOADS_PER_TILE * (NS - 2));
-            else wait_vmcnt_le(0);
-            tile_barrier();
-            if (it + NS - 1 < ntiles) issue_tile(it + NS - 1, (it + NS - 1) % NS);
-
-            lds_cptr kt;
-            if constexpr (FMT == DSA_KV_BF16) {
-                kt = L_raw + (it % NS) * RAW_SLOT;
-            } else {
-                lds_ptr dst = L_bf;
-                dequant_tile(L_raw + (it % NS) * RAW_SLOT, dst);
+            for (int s = 0; s < NPRE; ++s)
+                if (s < ntiles) issue_rows(load_rows(s), s);
+            if (NPRE < ntiles) gnext = load_rows(NPRE);
+        }
+        if constexpr (FP8) {
+            if (ntiles > 0) {
+                // tile 0 landed (tiles 1, 2 may still be in flight)
+                wait_tiles(min(ntiles, NPRE) - 1);
                 tile_barrier();
-                kt = dst;
+                dequant(RING, T0);
             }
-
-            // ---- S^T = K Q^T (32 rows x 32 heads) ----
-            __builtin_amdgcn_sched_barrier(0);
-            f32x16 sacc = f32x16{};
-            {
-                // K fragment of k-step ks: row lane%32, 16-byte chunk 2ks+hi.
-                // NoPE steps: one base + immediate; RoPE steps: swizzled chunk.
-                const int r = lane & 31;
-                lds_cptr kb = kt + r * NOPE_STRIDE + 16 * hi;
-                lds_cptr kr = kt + ROPE_BASE + r * ROPE_STRIDE;
-                const int sw = row_swz(r);
+            // Two tiles per trip, so that the buffer being read and the one
+            // being filled are distinct LDS objects in each step.
+            for (int it = 0; it < ntiles; it += 2) {
 #pragma unroll
-                for (int ks = 0; ks < D_QK / 16; ++ks) {
-                    constexpr int KS_NOPE = D_NOPE / 16;
-                    const bf16x8 a0 = ks < KS_NOPE ? lds_read_b128(kb + 32 * ks)
-                                                   : lds_read_b128(kr + 16 * ((2 * (ks - KS_NOPE) + hi) ^ sw));
-                    const bf16x8 qv = ks < QK_REG ? qf[ks < QK_REG ? ks : 0] : lds_read_b128(qr_lane + 32 * (ks - QK_REG));
-                    sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qv, sacc, 0, 0, 0);
-                    // (accumulator placement left to the register allocator)
-                }
-                // issue order: K-fragment reads run QK_PF ahead of the MFMAs
-                // (the last D_ROPE/16 steps also read their Q fragment)
-                constexpr int NK = D_QK / 16, QK_PF = 3;
-                __builtin_amdgcn_sched_group_barrier(0x100, QK_PF, 0);
-#pragma unroll
-                for (int i = 0; i < QK_REG - QK_PF; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                }
-#pragma unroll
-                for (int i = QK_REG - QK_PF; i < NK - QK_PF; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-                }
-#pragma unroll
-                for (int i = 0; i < QK_PF; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-
-            // ---- softmax numerators for this tile ----
-            // lane (hi, h32), reg r holds row 8*(r/4) + 4*hi + r%4 of head h32
-            float mx = -INFINITY;
-            const int row0 = it * TILE;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = 8 * (r >> 2) + 4 * hi + (r & 3);
-                sacc[r] = row0 + row < n_valid ? sacc[r] * p.scale_log2 : -INFINITY;
-                mx = fmaxf(mx, sacc[r]);
-            }
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            m_seen = fmaxf(m_seen, mx);
-            if (m_ref == -INFINITY) m_ref = mx;
-            if (__builtin_amdgcn_ballot_w64(mx > m_ref + RESTART_TAU) != 0 && lane == 0) s_restart = 1;
-            const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;
-            f32x8 pv0, pv1;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float e = __builtin_amdgcn_exp2f(sacc[r] - m_use);
-                l_lane += e;
-                if (r < 8) pv0[r] = e; else pv1[r - 8] = e;
-            }
-            if (ntiles == 1) {
-                // Every valid row is in this tile: normalise by the exact sum before the
-                // bf16 rounding of P, the order the reference uses (host.cc:448-451).
-                const float lt = l_lane + __shfl_xor(l_lane, 32, 64);
-#pragma unroll
-                for (int r = 0; r < 8; ++r) {
-                    pv0[r] = pv0[r] / lt;
-                    pv1[r] = pv1[r] / lt;
-                }
-            }
-            const bf16x8 pb0 = __builtin_convertvector(pv0, bf16x8);
-            const bf16x8 pb1 = __builtin_convertvector(pv1, bf16x8);
-
-            // ---- O^T += V^T P^T ----
-            __builtin_amdgcn_sched_barrier(0);
-            {
-                // Transposed read of rows R..R+3, columns d0..d0+15 (16-lane group):
-                // lane 4*rr+pp addresses row R+rr, columns d0+4pp..+3.  This wave
-                // needs R = 8a + 4hi (a = 2u, 2u+1) and d0 = 32mb + 16dh, so one
-                // per-lane base plus immediates covers every read.
-                const int g16 = lane >> 4, i16 = lane & 15;
-                const int rr = i16 >> 2, pp = i16 & 3;
-                const int dh = g16 & 1;
-                lds_cptr vb = kt + (4 * hi + rr) * NOPE_STRIDE + 32 * dh + 8 * pp;
-#pragma unroll
-                for (int mb = 0; mb < D_VO / 32; ++mb) {
-#pragma unroll
-                    for (int u = 0; u < 2; ++u) {
-                        const s16x4 va = lds_read_tr16(vb + 16 * u * NOPE_STRIDE + 64 * mb);
-                        const s16x4 vv = lds_read_tr16(vb + (16 * u + 8) * NOPE_STRIDE + 64 * mb);
-                        const bf16x8 a = __builtin_bit_cast(bf16x8, __builtin_shufflevector(va, vv, 0, 1, 2, 3, 4, 5, 6, 7));
-                        o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, u == 0 ? pb0 : pb1, o[mb], 0, 0, 0);
-                        pin_acc(o[mb]);
+                for (int h = 0; h < 2; ++h) {
+                    const int ii = it + h;
+                    if (ii < ntiles) {
+                        // tile ii+1 (dequantised in this step) must have landed
+                        wait_tiles(ii + 2 < ntiles ? 1 : 0);
+                        tile_barrier();
+                        step(ii, h == 0 ? T0 : T1, h == 0 ? T1 : T0);
                     }
                 }
-                // issue order: two transposed reads per MFMA, PV_PF fragments ahead
-                constexpr int NM = 2 * (D_VO / 32), PV_PF = 2;
-                __builtin_amdgcn_sched_group_barrier(0x100, 2 * PV_PF, 0);
-#pragma unroll
-                for (int i = 0; i < NM - PV_PF; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-                }
-#pragma unroll
-                for (int i = 0; i < PV_PF; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
-            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            int slot_cur = 0;        // ring slot of tile `it`
+            for (int it = 0; it < ntiles; ++it) {
+                wait_tiles(it + 1 < ntiles ? 1 : 0);
+                tile_barrier();
+                step(it, slot_buf(slot_cur), nullptr);
+                slot_cur = slot_cur == 2 ? 0 : slot_cur + 1;
+            }
         }
         // drain in-flight gathers before the ring can be reused or left
-        wait_vmcnt_le(0);
+        wait_vm<0>();
+        if (__builtin_amdgcn_ballot_w64(e_max > exp2f(L::TAU)) != 0 && lane == 0) s_misc[4] = 1;
         tile_barrier();
-        if (!s_restart) break;
-        tile_barrier();              // every wave has seen the flag
-        if (tid == 0) s_restart = 0;  // visible after the next tile barrier
-        m_ref = m_seen;
-        l_lane = 0.0f;
+        if (!s_misc[4]) break;
+        // new reference: an upper bound of every score (log2 units), per head
+        float lm = __builtin_amdgcn_logf(e_max);
+        lm = fmaxf(lm, __shfl_xor(lm, 32, 64));
+        m_ref += fmaxf(lm, 0.0f);
+        tile_barrier();              // every wave has read the flag
+        if (tid == 0) s_misc[4] = 0;  // visible after the next tile barrier
     }
 
     // ---- epilogue ----
+    // Wave w holds O for dims 128w..128w+127 of all heads; the softmax sums
+    // and references are per head, owned by the head's QK wave: exchange them.
     const float l = l_lane + __shfl_xor(l_lane, 32, 64);
     const bool has = l > 0.0f;
-    const float inv = has ? (ntiles == 1 ? 1.0f : 1.0f / l) : 0.0f;  // one tile: P was normalised
     const int64_t qrow = (int64_t)b * p.s_q + t;
+    LDS_AS float* const s_l = (LDS_AS float*)PX;      // P buffer is free now
+    if (hi == 0) s_l[head] = has ? (ntiles == 1 ? 1.0f : 1.0f / l) : 0.0f;   // one tile: P is normalised
+    if (hi == 0) {
+        const float lse_v = (m_ref + __builtin_amdgcn_logf(l)) * LN2;
+        if (p.part_o == nullptr) {
+            if (p.lse) p.lse[qrow * HEADS + head] = has ? lse_v : INFINITY;
+        } else {
+            p.part_lse[((int64_t)split * p.B * p.s_q + qrow) * HEADS + head] = has ? lse_v : -FLT_MAX;
+        }
+    }
+    __syncthreads();
+    float inv[NWAVE];
+#pragma unroll
+    for (int h = 0; h < NWAVE; ++h) inv[h] = s_l[32 * h + r32];
+    const int d0 = 128 * wave + 4 * hi;   // this lane's first output dim in block (m, g)
     if (p.part_o == nullptr) {
-        __bf16* op = p.out + (int64_t)b * p.o_sb + (int64_t)t * p.o_st + (int64_t)head * p.o_sh;
 #pragma unroll
-        for (int mb = 0; mb < D_VO / 32; ++mb) {
+        for (int h = 0; h < NWAVE; ++h) {
+            __bf16* op = p.out + (int64_t)b * p.o_sb + (int64_t)t * p.o_st + (int64_t)(32 * h + r32) * p.o_sh + d0;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const f32x4 v4 = {o[mb][4 * g] * inv, o[mb][4 * g + 1] * inv, o[mb][4 * g + 2] * inv,
-                                  o[mb][4 * g + 3] * inv};
-                typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-                const bf16x4 bv = __builtin_convertvector(v4, bf16x4);
-                *reinterpret_cast<u32x2*>(op + 32 * mb + 8 * g + 4 * hi) = __builtin_bit_cast(u32x2, bv);
+            for (int m = 0; m < 4; ++m) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x16& a = o[4 * m + h];
+                    const f32x4 v4 = {a[4 * g] * inv[h], a[4 * g + 1] * inv[h], a[4 * g + 2] * inv[h],
+                                      a[4 * g + 3] * inv[h]};
+                    const bf16x4 bv = __builtin_convertvector(v4, bf16x4);
+                    *reinterpret_cast<u32x2*>(op + 32 * m + 8 * g) = __builtin_bit_cast(u32x2, bv);
+                }
             }
         }
-        if (p.lse && hi == 0)
-            p.lse[qrow * HEADS + head] = has ? (m_ref + __builtin_amdgcn_logf(l)) * LN2 : INFINITY;
     } else {
-        const int64_t prow = ((int64_t)split * p.B * p.s_q + qrow) * HEADS + head;
-        float* op = p.part_o + prow * D_VO;
 #pragma unroll
-        for (int mb = 0; mb < D_VO / 32; ++mb) {
+        for (int h = 0; h < NWAVE; ++h) {
+            const int64_t prow = ((int64_t)split * p.B * p.s_q + qrow) * HEADS + 32 * h + r32;
+            float* op = p.part_o + prow * D_VO + d0;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const f32x4 v4 = {o[mb][4 * g] * inv, o[mb][4 * g + 1] * inv, o[mb][4 * g + 2] * inv,
-                                  o[mb][4 * g + 3] * inv};
-                *reinterpret_cast<f32x4*>(op + 32 * mb + 8 * g + 4 * hi) = v4;
+            for (int m = 0; m < 4; ++m) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x16& a = o[4 * m + h];
+                    const f32x4 v4 = {a[4 * g] * inv[h], a[4 * g + 1] * inv[h], a[4 * g + 2] * inv[h],
+                                      a[4 * g + 3] * inv[h]};
+                    *reinterpret_cast<f32x4*>(op + 32 * m + 8 * g) = v4;
+                }
             }
         }
-        if (hi == 0) p.part_lse[prow] = has ? (m_ref + __builtin_amdgcn_logf(l)) * LN2 : -FLT_MAX;
     }
 }
 
