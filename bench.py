@@ -131,6 +131,19 @@ def make_prefill(cfg, dev, seed=2031):
     return dict(q=q, kv=kv, idx=idx)
 
 
+def prefill_step(p, dev):
+    """(step, buffers) for one c5 prefill call through the C ABI."""
+    import torch
+    from opfoundry_amd import dsa
+    N = p["q"].shape[0]
+    pout = torch.empty((N, H, D_VO), dtype=torch.bfloat16, device=dev)
+    plse = torch.empty((N, H), dtype=torch.float32, device=dev)
+    a = dsa.make_prefill_args(p["q"], p["kv"], p["idx"], SM_SCALE, pout, plse)
+    nbytes = dsa.prefill_workspace_size(a)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes else None
+    return prepared_prefill(a, ws), (pout, plse, a, ws)
+
+
 def count_valid(d) -> int:
     import torch
     idx = d["idx"].long()
@@ -140,6 +153,54 @@ def count_valid(d) -> int:
     L = d["seq_lens"].long().view(B, 1, 1)
     hi = L - s_q + torch.arange(s_q, device=idx.device).view(1, s_q, 1) + 1 if d["causal"] else L
     return int(((idx >= 0) & (idx < torch.minimum(L, hi))).sum())
+
+
+def prepared_decode(a, ws):
+    """One decode step as a direct C-ABI call with arguments built once: the timed loop
+    measures the library, not Python argument checking."""
+    import ctypes
+    import torch
+    from opfoundry_amd.abi import check, load_library
+    fn = load_library().dsa_mla_decode
+    ap, wp, wb = ctypes.byref(a), ws.data_ptr(), ws.numel()
+    st = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        rc = fn(ap, wp, wb, st)
+        if rc:
+            check(rc, "dsa_mla_decode")
+    return step
+
+
+def prepared_prefill(a, ws):
+    import ctypes
+    import torch
+    from opfoundry_amd.abi import check, load_library
+    fn = load_library().dsa_mla_prefill
+    ap = ctypes.byref(a)
+    wp, wb = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
+    st = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        rc = fn(ap, wp, wb, st)
+        if rc:
+            check(rc, "dsa_mla_prefill")
+    return step
+
+
+def profiled_traffic(name):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 PMC summary
+    profiles/<name>: the line 'traffic_bytes_per_launch: N' (FETCH_SIZE and
+    WRITE_SIZE scaled by a plain copy's reading).  None if there is no such summary."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 # ------------------------------------------------------------------ timing
@@ -281,13 +342,9 @@ def main():
     if cfg["kind"] == "prefill":
         if not args.kernel_only:
             ap.error("--config c5 is reported inside the default JSON line; use it with --kernel-only")
-        from opfoundry_amd import dsa
         log("building c5 prefill inputs")
         p = make_prefill(cfg, dev)
-        pout = torch.empty((p["q"].shape[0], H, D_VO), dtype=torch.bfloat16, device=dev)
-        plse = torch.empty((p["q"].shape[0], H), dtype=torch.float32, device=dev)
-        ms = time_steps(lambda: dsa.mla_prefill(p["q"], p["kv"], p["idx"], SM_SCALE, pout, plse),
-                        args.steps, args.warmup)
+        ms = time_steps(prefill_step(p, dev)[0], args.steps, args.warmup)
         print(json.dumps({"config": args.config, "ms_per_step": ms}))
         return
 
@@ -303,7 +360,7 @@ def main():
     ns = dsa.decode_num_splits(a)
     ws_bytes = dsa.decode_workspace_size(a)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    step = lambda: decode_call(d, splits, out, lse, ws)  # noqa: E731
+    step = prepared_decode(a, ws)
 
     log(f"timing {args.steps} steps after {args.warmup} warm-up (splits={ns})")
     ms = time_steps(step, args.steps, args.warmup)
@@ -332,7 +389,7 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp8_e4m3 KV -> f16 MFMA, f32 accumulate" if cfg["fp8"] else "bf16 MFMA, f32 accumulate",
         "data": "synthetic",
         "config": {"workload": f"{args.config}: {NAMES[args.config]}", "kv_format":
                    "fp8_e4m3_656B" if cfg["fp8"] else "bf16_1152B", "num_splits": ns,
@@ -340,12 +397,14 @@ def main():
         "hbm_TBps": round(alg_bytes / (ms * 1e-3) / 1e12, 3),
         "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": profiled_traffic(f"dsa_mla_fwd_{'fp8' if cfg['fp8'] else 'bf16'}_"
+                                                 f"{args.config}_traffic.txt"),
                      "kernel": "dsa_mla_fwd_kernel<fp8>" if cfg["fp8"] else "dsa_mla_fwd_kernel<bf16>",
                      "kernel_avg_us": round(dom_ms * 1e3, 3), "alg_bytes": alg_bytes,
                      "mfma_frac": round(flops / (dom_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)},
     }
-    del out, lse, ws
+    del out, lse, ws, step, a
 
     if not args.no_cpu:
         log("CPU baseline (oracle) on a bounded sample")
@@ -356,18 +415,21 @@ def main():
     if not args.no_prefill:
         log("building c5 prefill inputs")
         p = make_prefill(CONFIGS["c5"], dev)
-        pout = torch.empty((p["q"].shape[0], H, D_VO), dtype=torch.bfloat16, device=dev)
-        plse = torch.empty((p["q"].shape[0], H), dtype=torch.float32, device=dev)
-        pstep = lambda: dsa.mla_prefill(p["q"], p["kv"], p["idx"], SM_SCALE, pout, plse)  # noqa
+        pstep, keep = prefill_step(p, dev)
         psteps = max(3, args.steps // 5)
         pms = time_steps(pstep, psteps, 2)
+        pk_ms = kernel_avg_ms(pstep, psteps)
+        del keep
         pV = int((p["idx"] >= 0).sum())
         pfl = FLOP_PER_PAIR * pV
         res["prefill"] = {"workload": f"c5: {NAMES['c5']}", "ms_per_step": round(pms, 4),
                           "tflops": round(pfl / (pms * 1e-3) / 1e12, 1), "valid_pairs": pV,
-                          "roofline": {"bound": "mfma", "achieved": round(pfl / (pms * 1e-3) / 1e12, 1),
+                          "roofline": {"bound": "mfma", "achieved": round(pfl / (pk_ms * 1e-3) / 1e12, 1),
                                        "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                       "frac": round(pfl / (pms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}}
+                                       "frac": round(pfl / (pk_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                                       "traffic": profiled_traffic("dsa_mla_fwd_bf16_c5_traffic.txt"),
+                                       "kernel": "dsa_mla_fwd_kernel<bf16>",
+                                       "kernel_avg_us": round(pk_ms * 1e3, 1)}}
         if not args.no_cpu:
             res["prefill"]["cpu_baseline"] = cpu_baseline_prefill(p, args.cpu_prefill_sample, pV)
     print(json.dumps(res))

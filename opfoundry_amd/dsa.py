@@ -178,6 +178,13 @@ def make_prefill_args(q, kv, indices, sm_scale, out, lse, *, causal=False, causa
     return a
 
 
+def prefill_workspace_size(args: PrefillArgs) -> int:
+    n = ctypes.c_size_t(0)
+    check(load_library().dsa_mla_prefill_workspace_size(ctypes.byref(args), ctypes.byref(n)),
+          "dsa_mla_prefill_workspace_size")
+    return n.value
+
+
 def mla_prefill(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor, sm_scale: float,
                 out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None, *,
                 causal: bool = False, causal_offset: int = 0,
@@ -193,14 +200,11 @@ def mla_prefill(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor, sm_sca
         lse = torch.empty((N, H), dtype=torch.float32, device=q.device)
     a = make_prefill_args(q, kv, indices, sm_scale, out, lse, causal=causal,
                           causal_offset=causal_offset)
-    n = ctypes.c_size_t(0)
-    lib = load_library()
-    check(lib.dsa_mla_prefill_workspace_size(ctypes.byref(a), ctypes.byref(n)),
-          "dsa_mla_prefill_workspace_size")
-    if n.value and (workspace is None or workspace.numel() * workspace.element_size() < n.value):
-        workspace = torch.empty(n.value, dtype=torch.uint8, device=q.device)
-    check(lib.dsa_mla_prefill(ctypes.byref(a), _ptr(workspace) if n.value else None, n.value,
-                              _stream(stream)), "dsa_mla_prefill")
+    nbytes = prefill_workspace_size(a)
+    if nbytes and (workspace is None or workspace.numel() * workspace.element_size() < nbytes):
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    check(load_library().dsa_mla_prefill(ctypes.byref(a), _ptr(workspace) if nbytes else None,
+                                         nbytes, _stream(stream)), "dsa_mla_prefill")
     return out, lse
 
 
