@@ -20,9 +20,13 @@ INCLUDE = os.path.normpath(os.path.join(PKG_DIR, "..", "include"))
 # Packed-fp32 VALU ops are disabled for all device code: only ordinary
 # scalar / float2 code is written and the compiler may not fuse it into
 # v_pk_*_f32.  The host pass warns that it does not know the feature.
+# MFMAs the compiler emits take their accumulators in VGPRs
+# (amdgpu-mfma-vgpr-form): the AGPR file holds the O accumulators, which the
+# kernel binds there itself.
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-function",
 ]
 

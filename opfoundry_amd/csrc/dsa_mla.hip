@@ -120,9 +120,16 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 0xF) | ((N >> 4) << 14));
 }
 
-// Keep an MFMA accumulator tile in AGPRs (an empty asm with an AGPR operand):
-// the O accumulators live there for the whole kernel.
-__device__ __forceinline__ void pin_acc(f32x16& v) { asm("" : "+a"(v)); }
+// Wait states between the O MFMAs (inline asm) and VALU accesses of O: 24
+// covers a VALU read or write after the last 8-pass MFMA and an MFMA after a
+// VALU write.  Every O tile is an in/out operand, so no access of O moves
+// across it.
+__device__ __forceinline__ void o_fence(f32x16 (&o)[16]) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+                 : "+a"(o[0]), "+a"(o[1]), "+a"(o[2]), "+a"(o[3]), "+a"(o[4]), "+a"(o[5]),
+                   "+a"(o[6]), "+a"(o[7]), "+a"(o[8]), "+a"(o[9]), "+a"(o[10]), "+a"(o[11]),
+                   "+a"(o[12]), "+a"(o[13]), "+a"(o[14]), "+a"(o[15]));
+}
 // Opaque copy: stops the compiler from hoisting per-lane address math out of
 // the tile loop (which would pin dozens of loop-invariant VGPRs).
 __device__ __forceinline__ int opaque(int v) {
@@ -208,6 +215,21 @@ __device__ __forceinline__ f32x16 mfma_bf16(u32x4 a, u32x4 b, f32x16 c) {
 __device__ __forceinline__ f32x16 mfma_f16(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// O += A B on an AGPR accumulator.  Inline asm, so the O accumulators are
+// bound to AGPRs for the whole kernel while every other MFMA (QK^T) keeps its
+// accumulator in VGPRs: the AGPR file is exactly the 16 O tiles, and an
+// accumulator of the compiler's choosing there would displace one of them.
+// The compiler does not see these as MFMAs, so the wait states it would add
+// are written out: "s_nop 1" covers a VALU write of an operand just before
+// (2 wait states); o_fence() covers VALU accesses of O around the loop.
+template <bool F16>
+__device__ __forceinline__ void mfma_o(f32x16& acc, u32x4 a, u32x4 b) {
+    if constexpr (F16)
+        asm("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+    else
+        asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 
 // bf16 pair -> fp16 pair.  Exact for |x| in [2^-14, 65504]; smaller values go
@@ -438,16 +460,19 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // ---- online softmax state (fixed reference max) ----
     // p = exp2(s*c - m_ref) with m_ref fixed for the whole pass (the first
     // tile's maximum per head), so the O accumulators are never rescaled in
-    // the loop.  If some p exceeds 2^TAU (a later score grew past the range of
-    // the P format) the restart flag is raised; the workgroup then reruns the
-    // tiles with m_ref raised by log2 of the largest p seen, an upper bound of
-    // the true maximum.
+    // the loop.  The pass also tracks the largest raw score per head; if it
+    // exceeds the reference by more than TAU (log2 units: some p left the
+    // range of the P format) the workgroup reruns its tiles once with m_ref
+    // set to that exact maximum, where every p <= 1.  A second rerun never
+    // happens (the maximum is exact), and none is allowed, so no input -
+    // NaN, infinities or scores far beyond fp32's integer range included -
+    // can keep the loop going.
     const float c_s = p.scale_log2;
     // O^T accumulators of this wave: dims 128*wave + 32*m + (0..31) for the
     // 32 heads 32*h + (0..31): o[4*m + h] (the PV step is split by output
     // dims across the waves, so each gathered V value is read by one wave).
     f32x16 o[D_VO / 32];
-    float m_ref = 0.0f, l_lane = 0.0f, e_max = 0.0f;
+    float m_ref = 0.0f, l_lane = 0.0f, s_max = -INFINITY;
     constexpr int NPRE = FP8 ? 3 : 2;       // tiles in flight before the loop
     GatherRows gnext;
 #pragma unroll
@@ -562,14 +587,14 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             float e[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], c_s, -m_ref));
-            float lt = 0.0f, em = 0.0f;
+            float lt = 0.0f, sm = -INFINITY;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 lt += e[r];
-                em = fmaxf(em, e[r]);
+                sm = fmaxf(sm, sacc[r]);
             }
             l_lane += lt;
-            e_max = fmaxf(e_max, em);
+            s_max = fmaxf(s_max, sm);
             lds_st<u32x4>(PX + ((0 * NWAVE + wave) * 64 + ln) * 16, to_p(e));
             lds_st<u32x4>(PX + ((1 * NWAVE + wave) * 64 + ln) * 16, to_p(e + 8));
         }
@@ -603,10 +628,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                     __builtin_amdgcn_sched_barrier(0);
                     const u32x4 va_nxt = m + 1 < 4 ? v_frag(u, m + 1) : va_cur;
 #pragma unroll
-                    for (int h = 0; h < NWAVE; ++h) {
-                        o[4 * m + h] = FP8 ? mfma_f16(va_cur, pbf[h], o[4 * m + h]) : mfma_bf16(va_cur, pbf[h], o[4 * m + h]);
-                        pin_acc(o[4 * m + h]);
-                    }
+                    for (int h = 0; h < NWAVE; ++h) mfma_o<FP8>(o[4 * m + h], va_cur, pbf[h]);
                     if constexpr (FP8) {
                         // piece j: loads in MFMA group j, conversion + store in group j+1
                         const int j = step_i;
@@ -634,12 +656,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 
     for (int pass = 0;; ++pass) {
 #pragma unroll
-        for (int mb = 0; mb < D_VO / 32; ++mb) {
-            o[mb] = f32x16{};
-            pin_acc(o[mb]);
-        }
+        for (int mb = 0; mb < D_VO / 32; ++mb) o[mb] = f32x16{};
+        o_fence(o);
         l_lane = 0.0f;
-        e_max = 0.0f;
+        s_max = -INFINITY;
         first_tile = pass == 0;
         if (pass > 0) {
 #pragma unroll
@@ -679,13 +699,14 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         }
         // drain in-flight gathers before the ring can be reused or left
         wait_vm<0>();
-        if (__builtin_amdgcn_ballot_w64(e_max > exp2f(L::TAU)) != 0 && lane == 0) s_misc[4] = 1;
+        o_fence(o);
+        // per head: the largest score of the pass (log2 units); NaN compares false
+        const float top = fmaxf(s_max, __shfl_xor(s_max, 32, 64)) * c_s;
+        if (pass == 0 && __builtin_amdgcn_ballot_w64(top - m_ref > L::TAU) != 0 && lane == 0) s_misc[4] = 1;
         tile_barrier();
         if (!s_misc[4]) break;
-        // new reference: an upper bound of every score (log2 units), per head
-        float lm = __builtin_amdgcn_logf(e_max);
-        lm = fmaxf(lm, __shfl_xor(lm, 32, 64));
-        m_ref += fmaxf(lm, 0.0f);
+        // new reference: the exact maximum of every score of the head
+        m_ref = fmaxf(m_ref, top);
         tile_barrier();              // every wave has read the flag
         if (tid == 0) s_misc[4] = 0;  // visible after the next tile barrier
     }
