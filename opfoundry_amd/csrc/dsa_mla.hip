@@ -61,6 +61,7 @@ constexpr int TILE_BYTES = ROPE_OFF + TILE * 128;    // 38912
 constexpr int RAW_BYTES = TILE * FP8_ROW;            // raw fp8 tile, rows back to back (20992)
 constexpr int FP8_CHUNKS = RAW_BYTES / 16;           // 16-byte chunks of a raw tile (1312)
 constexpr int FP8_LOADS = (FP8_CHUNKS + 63) / 64;    // wave-wide loads per raw tile (21)
+constexpr int RAW_STRIDE = FP8_LOADS * 1024;         // raw slot padded to whole loads (21504)
 constexpr int FP8_LPW = (FP8_LOADS + NWAVE - 1) / NWAVE;  // loads of wave 0 (6); the others 5
 constexpr int BF16_LPW = TILE / NWAVE + 1;           // 8 NoPE rows + one 8-row RoPE block
 constexpr int FP8_SCALE_OFF = D_NOPE;                // 4 fp32 scales
@@ -74,7 +75,7 @@ __device__ __forceinline__ int rope_sw(int r) { return (r >> 1) & 7; }
 template <int FMT>
 struct Lay {
     static constexpr bool FP8 = FMT == DSA_KV_FP8_656;
-    static constexpr int RING_BYTES = FP8 ? 3 * RAW_BYTES : TILE_BYTES;
+    static constexpr int RING_BYTES = FP8 ? 3 * RAW_STRIDE : TILE_BYTES;
     static constexpr int LPW = FP8 ? FP8_LPW : BF16_LPW;  // max DMA loads per wave per tile
     // p = exp2(s - m_ref) may grow to 2^TAU over the reference before a
     // restart: fp16 P (fp8 cache) is finite below 2^16, bf16 P below 2^128.
@@ -363,8 +364,9 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         } else {
 #pragma unroll
             for (int i = 0; i < FP8_LPW; ++i) {
-                const int c16 = 64 * (wave + NWAVE * i) + ln;      // linear chunk of the raw tile
-                g.r[i] = rows[min((c16 * 1599) >> 16, TILE - 1)];  // c16 / 41
+                const unsigned c16 = 64 * (wave + NWAVE * i) + ln;   // linear chunk of the raw tile
+                const unsigned rt = __umul24(c16, 1599u) >> 16;     // c16 / 41
+                g.r[i] = rows[rt < TILE - 1 ? rt : TILE - 1];
             }
             g.rope = 0;
         }
@@ -387,11 +389,15 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             }
         } else {
             if (i < my_loads) {
+                // Lane chunk c16 = 41 * rt + c of the raw tile.  The last load
+                // runs past the tile's 1312 chunks: those lanes read chunks of
+                // row 31 (rt clamped to 31 when the row id was fetched, c
+                // < 32) into the slot's padding, so no lane is masked off.
                 const int k = wave + NWAVE * i;
-                const int c16 = 64 * k + ln;
-                const int c = c16 - 41 * ((c16 * 1599) >> 16);
-                const unsigned char* src = p.kv + (int64_t)g.r[i] * FP8_ROW + 16 * c;
-                if (c16 < FP8_CHUNKS) lds_dma16(src, RING + slot * RAW_BYTES + 1024 * k);
+                const unsigned c16 = 64 * k + ln;
+                const unsigned c = c16 - 41u * (__umul24(c16, 1599u) >> 16);
+                const uint64_t ch = (uint64_t)(uint32_t)g.r[i] * 41u + c;   // 16-byte chunk of the cache
+                lds_dma16(p.kv + (ch << 4), RING + slot * RAW_STRIDE + 1024 * k);
             }
         }
     };
@@ -533,6 +539,11 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         const int issue_slot = FP8 ? it % 3 : (it + 2) % 3;
         const GatherRows gcur = gnext;
         __builtin_amdgcn_sched_barrier(0);
+        // Gathers of tile it+NPRE, all at once: the tile barrier just before
+        // has drained this wave's LDS accesses, and an LDS-DMA load issued
+        // while LDS reads are in flight holds the wave far longer.
+        if (do_issue) issue_rows(gcur, issue_slot);
+        __builtin_amdgcn_sched_barrier(0);
         u32x4 kb[KPF];
 #pragma unroll
         for (int i = 0; i < KPF; ++i) kb[i] = lds_ld<u32x4>(k_addr(i));
@@ -543,7 +554,6 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             if (FP8 && ks < KS_NOPE) sacc = mfma_f16(kb[ks % KPF], qf[ks], sacc);
             else sacc = mfma_bf16(kb[ks % KPF], qf[ks], sacc);
             if (ks + KPF < KS_ALL) kb[ks % KPF] = lds_ld<u32x4>(k_addr(ks + KPF));
-            if (FP8 && ks % 6 == 1 && ks / 6 < FP8_LPW && do_issue) issue_one(gcur, issue_slot, ks / 6);
         }
         __builtin_amdgcn_sched_barrier(0);
         // row ids of the tile issued in the next step
@@ -609,7 +619,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             const int vx = 2 * (g16 & 1) + (pp >> 1);
             const lds_cptr v_a = kt + (4 * lhi + rr) * NOPE_STRIDE + 16 * (vx ^ lhi) + 8 * (pp & 1) + 256 * wave;
             const lds_cptr v_b = kt + (4 * lhi + rr + 8) * NOPE_STRIDE + 16 * (vx ^ (lhi + 2)) + 8 * (pp & 1) + 256 * wave;
-            const lds_cptr draw = FP8 ? RING + ((it + 1) % 3) * RAW_BYTES : kt;
+            const lds_cptr draw = FP8 ? RING + ((it + 1) % 3) * RAW_STRIDE : kt;
             auto v_frag = [&](int u, int m) -> u32x4 {
                 const s16x4 va = lds_read_tr16(v_a + 16 * u * NOPE_STRIDE + 64 * m);
                 const s16x4 vb = lds_read_tr16(v_b + 16 * u * NOPE_STRIDE + 64 * m);
@@ -634,10 +644,6 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                         const int j = step_i;
                         dq[j & 1] = deq_load(draw, j);
                         if (j >= 1) deq_store(nxt, j - 1, dq[(j - 1) & 1]);
-                    } else if (do_issue) {
-                        // gathers of tile it+2: one load per MFMA group (two in the first)
-                        if (step_i == 0) issue_one(gcur, issue_slot, 8);
-                        issue_one(gcur, issue_slot, step_i);
                     }
                     va_cur = va_nxt;
                     ++step_i;
