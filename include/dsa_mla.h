@@ -148,6 +148,51 @@ int dsa_mla_combine(const float* partial_o, const float* partial_lse, int32_t nu
                     float* lse, void* stream);
 
 /*
+ * Sparse MLA decode, CSR form: the argument set of the reference kernel
+ * (opus_mla_decode_kargs, opus_attn/dsa_v32/common/defs.h:109-131, minus the
+ * work / plan pointers the library plans itself), so a dsa_v32-style harness
+ * can call it in place of mla_decode_launch_pipeline
+ * (opus_attn/dsa_v32/common/host.cc:114-138).
+ * q        : bf16 [B * s_q, H, 576]; query row i = b * s_q + t at
+ *            q + i * stride_q_b + h * stride_q_h (elements)
+ * kv       : [total_tokens, row] in kv_format; page size 1, so an index is a
+ *            physical cache row (bf16 rows are 576 elements apart)
+ * kv_indptr: int32 [B + 1]; kv_indices: int32 rows.  Query token t of batch b
+ *            attends kv_indices[kv_indptr[b] + p] for
+ *            0 <= p < kv_indptr[b + 1] - kv_indptr[b] - (s_q - 1 - t)
+ *            (count-based MTP causality, host.cc:482,526).  A row outside
+ *            [0, total_tokens) is skipped; an empty range gives O = 0 and
+ *            LSE = +inf (host.cc:486-489).
+ * out      : bf16 [B * s_q, H, 512] at out + i * stride_o_b + h * stride_o_h
+ * lse      : fp32 [B * s_q, H] dense (may be NULL)
+ * max_kv_len: an upper bound of kv_indptr[b + 1] - kv_indptr[b] over b (the
+ *            host cannot read the device lists; the split plan uses it)
+ */
+typedef struct {
+    const void* q;
+    const void* kv;
+    void* out;
+    float* lse;
+    const int32_t* kv_indptr;
+    const int32_t* kv_indices;
+    int32_t B, s_q, H;
+    int32_t total_tokens;
+    int32_t stride_q_b, stride_q_h;
+    int32_t stride_o_b, stride_o_h;
+    int32_t kv_format;
+    int32_t max_kv_len;
+    int32_t num_splits;          /* 0 = automatic */
+    float softmax_scale;
+} dsa_mla_decode_csr_args;
+
+/* Workspace bytes dsa_mla_decode_csr needs (0 when unsplit). */
+int dsa_mla_decode_csr_workspace_size(const dsa_mla_decode_csr_args* args, size_t* bytes);
+
+/* Launch the CSR decode (kernel + split combine) on `stream`. */
+int dsa_mla_decode_csr(const dsa_mla_decode_csr_args* args, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/*
  * Sparse MLA prefill (per-query top-k over one KV pool).
  * q       : bf16 [N, H, 576] addressed by q_stride_{n,h}
  * kv      : [kv_rows, row] in kv_format

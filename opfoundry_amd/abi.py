@@ -36,6 +36,8 @@ EXPORTED_SYMBOLS = (
     "dsa_mla_decode_workspace_size",
     "dsa_mla_decode_num_splits",
     "dsa_mla_decode",
+    "dsa_mla_decode_csr_workspace_size",
+    "dsa_mla_decode_csr",
     "dsa_mla_combine",
     "dsa_mla_prefill_workspace_size",
     "dsa_mla_prefill",
@@ -44,7 +46,7 @@ EXPORTED_SYMBOLS = (
     "dsa_mla_abi_version",
 )
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -65,6 +67,19 @@ class DecodeArgs(ctypes.Structure):
         ("lse", _vp),
         ("B", _i32), ("s_q", _i32), ("H", _i32), ("topk", _i32),
         ("num_splits", _i32), ("causal", _i32), ("sm_scale", ctypes.c_float),
+    ]
+
+
+class CsrArgs(ctypes.Structure):
+    """dsa_mla_decode_csr_args (include/dsa_mla.h): the reference's opus_mla_decode_kargs fields."""
+
+    _fields_ = [
+        ("q", _vp), ("kv", _vp), ("out", _vp), ("lse", _vp),
+        ("kv_indptr", _vp), ("kv_indices", _vp),
+        ("B", _i32), ("s_q", _i32), ("H", _i32), ("total_tokens", _i32),
+        ("stride_q_b", _i32), ("stride_q_h", _i32), ("stride_o_b", _i32), ("stride_o_h", _i32),
+        ("kv_format", _i32), ("max_kv_len", _i32), ("num_splits", _i32),
+        ("softmax_scale", ctypes.c_float),
     ]
 
 
@@ -106,6 +121,8 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.dsa_mla_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeArgs), sz]
     lib.dsa_mla_decode_num_splits.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.POINTER(_i32)]
     lib.dsa_mla_decode.argtypes = [ctypes.POINTER(DecodeArgs), _vp, ctypes.c_size_t, _vp]
+    lib.dsa_mla_decode_csr_workspace_size.argtypes = [ctypes.POINTER(CsrArgs), sz]
+    lib.dsa_mla_decode_csr.argtypes = [ctypes.POINTER(CsrArgs), _vp, ctypes.c_size_t, _vp]
     lib.dsa_mla_combine.argtypes = [_vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _vp]
     lib.dsa_mla_prefill_workspace_size.argtypes = [ctypes.POINTER(PrefillArgs), sz]
     lib.dsa_mla_prefill.argtypes = [ctypes.POINTER(PrefillArgs), _vp, ctypes.c_size_t, _vp]

@@ -175,6 +175,8 @@ struct FwdParams {
     int64_t seq_len_default;
     const int32_t* indices;
     int64_t idx_sb, idx_st;
+    const int32_t* kv_indptr;    // CSR form (NULL: top-k form): rows kv_indices[kv_indptr[b] + k]
+    const int32_t* kv_indices;
     __bf16* out;
     int64_t o_sb, o_st, o_sh;
     float* lse;
@@ -285,13 +287,29 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     }
 
     // ---- 1. resolve this split's index chunk into a compacted row list ----
+    // Top-k form: logical positions through the block table, bounded by
+    // seq_len and the causal rule.  CSR form: physical rows
+    // kv_indices[kv_indptr[b] + k] for k < kv_indptr[b+1] - kv_indptr[b] -
+    // (s_q - 1 - t), the reference's count-based MTP causality
+    // (opus_attn/dsa_v32/common/host.cc:524-526); a row outside the cache is
+    // skipped.
     const int k0 = split * p.chunk;
-    const int k1 = min(k0 + p.chunk, p.topk);
-    const int64_t Lq = p.seq_lens ? (int64_t)p.seq_lens[b] : p.seq_len_default;
-    int64_t jmax = Lq;
-    if (p.causal == 1) jmax = min(Lq, Lq - p.s_q + t + 1);
-    else if (p.causal == 2) jmax = min(Lq, (int64_t)b + p.causal_offset + 1);
-    const int32_t* idx = p.indices + (int64_t)b * p.idx_sb + (int64_t)t * p.idx_st;
+    int k1;
+    int64_t jmax = 0;
+    const int32_t* idx;
+    if (p.kv_indptr) {
+        const int64_t kb = p.kv_indptr[b];
+        const int64_t count = (int64_t)p.kv_indptr[b + 1] - kb - (p.s_q - 1 - t);
+        k1 = (int)min((int64_t)k0 + p.chunk, count);
+        idx = p.kv_indices + kb;
+    } else {
+        k1 = min(k0 + p.chunk, p.topk);
+        const int64_t Lq = p.seq_lens ? (int64_t)p.seq_lens[b] : p.seq_len_default;
+        jmax = Lq;
+        if (p.causal == 1) jmax = min(Lq, Lq - p.s_q + t + 1);
+        else if (p.causal == 2) jmax = min(Lq, (int64_t)b + p.causal_offset + 1);
+        idx = p.indices + (int64_t)b * p.idx_sb + (int64_t)t * p.idx_st;
+    }
 
     constexpr int PER_T = MAX_CHUNK / NTHR;  // 8 entries per thread
     int32_t rows_local[PER_T];
@@ -305,7 +323,8 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         }
 #pragma unroll
         for (int e = 0; e < PER_T; ++e) {
-            rows_local[e] = (int32_t)resolve_row(p, b, jmax, jv[e]);
+            rows_local[e] = p.kv_indptr ? (jv[e] >= 0 && (int64_t)jv[e] < p.kv_total_rows ? jv[e] : -1)
+                                        : (int32_t)resolve_row(p, b, jmax, jv[e]);
             cnt += rows_local[e] >= 0 ? 1 : 0;
         }
     }
@@ -925,7 +944,7 @@ int validate_decode(const dsa_mla_decode_args* a, int* ns_out, int* chunk_out) {
 }
 
 size_t decode_ws_bytes(const dsa_mla_decode_args* a, int ns) {
-    if (ns <= 1) return 0;
+    if (ns <= 1 || a->B == 0) return 0;
     const size_t rows = (size_t)a->B * a->s_q * HEADS;
     return (size_t)ns * rows * (D_VO + 1) * sizeof(float) + 256;
 }
@@ -946,11 +965,38 @@ int launch_combine(const float* po, const float* pl, int ns, int rows, int H, in
     return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_HIP;
 }
 
+int validate_csr(const dsa_mla_decode_csr_args* a, int* ns_out, int* chunk_out) {
+    if (!a) return DSA_ERR_NULL_POINTER;
+    if (a->B < 0 || a->s_q <= 0 || a->max_kv_len < 0 || a->total_tokens < 0) return DSA_ERR_BAD_SHAPE;
+    if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
+    if (a->kv_format != DSA_KV_BF16 && a->kv_format != DSA_KV_FP8_656) return DSA_ERR_BAD_FORMAT;
+    if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
+    const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q, a->max_kv_len);
+    const int chunk = a->max_kv_len == 0 ? 0 : (a->max_kv_len + ns - 1) / ns;
+    if (chunk > MAX_CHUNK) return a->num_splits ? DSA_ERR_BAD_SPLITS : DSA_ERR_UNSUPPORTED;
+    if (a->B > 0) {
+        if (!a->out || !a->kv_indptr) return DSA_ERR_NULL_POINTER;
+        if (a->max_kv_len > 0 && (!a->q || !a->kv || !a->kv_indices)) return DSA_ERR_NULL_POINTER;
+        if (a->stride_q_b < 0 || a->stride_q_h < 0 || a->stride_o_b < 0 || a->stride_o_h < 0)
+            return DSA_ERR_BAD_STRIDE;
+        if ((a->stride_q_h % 8) || (a->stride_q_b % 8) || (a->stride_o_h % 4) || (a->stride_o_b % 4))
+            return DSA_ERR_BAD_STRIDE;
+        if (((uintptr_t)a->q & 15) || ((uintptr_t)a->kv & 15) || ((uintptr_t)a->out & 7))
+            return DSA_ERR_BAD_STRIDE;
+    }
+    *ns_out = ns;
+    *chunk_out = chunk;
+    return DSA_OK;
+}
+size_t csr_ws_bytes(const dsa_mla_decode_csr_args* a, int ns) {
+    return ns <= 1 || a->B == 0 ? 0 : (size_t)ns * a->B * a->s_q * HEADS * (D_VO + 1) * sizeof(float) + 256;
+}
+
 }  // namespace
 
 extern "C" {
 
-int dsa_mla_abi_version(void) { return 1; }
+int dsa_mla_abi_version(void) { return 2; }
 
 const char* dsa_mla_strerror(int code) {
     switch (code) {
@@ -1025,6 +1071,46 @@ int dsa_mla_decode(const dsa_mla_decode_args* a, void* ws, size_t ws_bytes, void
                           a->o_stride_t, a->o_stride_h, a->lse, st);
 }
 
+int dsa_mla_decode_csr_workspace_size(const dsa_mla_decode_csr_args* a, size_t* bytes) {
+    if (!bytes) return DSA_ERR_NULL_POINTER;
+    int ns, chunk;
+    const int rc = validate_csr(a, &ns, &chunk);
+    if (rc) return rc;
+    *bytes = csr_ws_bytes(a, ns);
+    return DSA_OK;
+}
+int dsa_mla_decode_csr(const dsa_mla_decode_csr_args* a, void* ws, size_t ws_bytes, void* stream) {
+    int ns, chunk;
+    const int rc = validate_csr(a, &ns, &chunk);
+    if (rc) return rc;
+    const size_t need = csr_ws_bytes(a, ns);
+    if (need && (!ws || ws_bytes < need || ((uintptr_t)ws & 15))) return DSA_ERR_WORKSPACE;
+    if (a->B == 0) return DSA_OK;
+    hipStream_t st = (hipStream_t)stream;
+    FwdParams fp{};
+    fp.q = (const __bf16*)a->q;
+    fp.q_sb = (int64_t)a->s_q * a->stride_q_b; fp.q_st = a->stride_q_b; fp.q_sh = a->stride_q_h;
+    fp.kv = (const unsigned char*)a->kv;
+    fp.kv_total_rows = a->total_tokens;
+    fp.block_size = 1;
+    fp.seq_len_default = a->total_tokens;
+    fp.kv_indptr = a->kv_indptr;
+    fp.kv_indices = a->kv_indices;
+    fp.out = (__bf16*)a->out;
+    fp.o_sb = (int64_t)a->s_q * a->stride_o_b; fp.o_st = a->stride_o_b; fp.o_sh = a->stride_o_h;
+    fp.lse = a->lse;
+    fp.B = a->B; fp.s_q = a->s_q; fp.topk = a->max_kv_len; fp.chunk = chunk;
+    fp.scale_log2 = a->softmax_scale * LOG2E;
+    if (ns > 1) {
+        const size_t rows = (size_t)a->B * a->s_q * HEADS;
+        fp.part_o = (float*)ws;
+        fp.part_lse = (float*)((char*)ws + (size_t)ns * rows * D_VO * sizeof(float));
+    }
+    int r = launch_fwd(fp, a->kv_format, a->B, a->s_q, ns, st);
+    if (r || ns == 1) return r;
+    return launch_combine(fp.part_o, fp.part_lse, ns, a->B * a->s_q, HEADS, a->s_q, a->out, fp.o_sb, fp.o_st,
+                          fp.o_sh, a->lse, st);
+}
 int dsa_mla_combine(const float* po, const float* pl, int32_t ns, int32_t rows, int32_t H, void* out,
                     int64_t o_sr, int64_t o_sh, float* lse, void* stream) {
     if (rows < 0 || H <= 0) return DSA_ERR_BAD_SHAPE;

@@ -132,6 +132,63 @@ def mla_decode(q: torch.Tensor, kv_cache: torch.Tensor, indices: torch.Tensor, s
     return out, lse
 
 
+def make_decode_csr_args(q, kv, kv_indptr, kv_indices, sm_scale, out, lse, *, s_q=1,
+                         max_kv_len=None, num_splits=0):
+    """CSR-form arguments: q [B*s_q, H, 576], kv [total_tokens, row], kv_indptr int32 [B+1],
+    kv_indices int32 (physical rows, page size 1)."""
+    total_q, H, D = q.shape
+    if D != abi.D_QK or q.stride(2) != 1:
+        raise ValueError("q must be [B*s_q, H, 576] with a dense last dim")
+    if total_q % s_q:
+        raise ValueError("q rows must be B * s_q")
+    fmt, rows = kv_format_of(kv)
+    B = kv_indptr.numel() - 1
+    if B * s_q != total_q:
+        raise ValueError("kv_indptr must have B + 1 entries with B * s_q == q.shape[0]")
+    if max_kv_len is None:
+        max_kv_len = int((kv_indptr[1:] - kv_indptr[:-1]).max()) if B > 0 else 0
+    a = abi.CsrArgs()
+    a.q, a.kv, a.out, a.lse = _ptr(q), _ptr(kv), _ptr(out), _ptr(lse)
+    a.kv_indptr, a.kv_indices = _ptr(kv_indptr), _ptr(kv_indices)
+    a.B, a.s_q, a.H, a.total_tokens = B, s_q, H, rows
+    a.stride_q_b, a.stride_q_h = q.stride(0), q.stride(1)
+    a.stride_o_b, a.stride_o_h = out.stride(0), out.stride(1)
+    a.kv_format = fmt
+    a.max_kv_len = int(max_kv_len)
+    a.num_splits = int(num_splits)
+    a.softmax_scale = float(sm_scale)
+    return a
+
+
+def mla_decode_csr(q: torch.Tensor, kv: torch.Tensor, kv_indptr: torch.Tensor,
+                   kv_indices: torch.Tensor, sm_scale: float, out: Optional[torch.Tensor] = None,
+                   lse: Optional[torch.Tensor] = None, *, s_q: int = 1,
+                   max_kv_len: Optional[int] = None, num_splits: int = 0,
+                   workspace: Optional[torch.Tensor] = None,
+                   stream=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Sparse MLA decode in the reference's CSR form (kv_indptr / kv_indices, page size 1,
+    count-based MTP causality); returns (out bf16 [B*s_q, H, 512], lse fp32 [B*s_q, H])."""
+    _need(q, torch.bfloat16, "q")
+    _need(kv_indptr, torch.int32, "kv_indptr")
+    _need(kv_indices, torch.int32, "kv_indices")
+    total_q, H, _ = q.shape
+    if out is None:
+        out = torch.empty((total_q, H, abi.D_VO), dtype=torch.bfloat16, device=q.device)
+    if lse is None:
+        lse = torch.empty((total_q, H), dtype=torch.float32, device=q.device)
+    a = make_decode_csr_args(q, kv, kv_indptr, kv_indices, sm_scale, out, lse, s_q=s_q,
+                             max_kv_len=max_kv_len, num_splits=num_splits)
+    lib = load_library()
+    n = ctypes.c_size_t(0)
+    check(lib.dsa_mla_decode_csr_workspace_size(ctypes.byref(a), ctypes.byref(n)),
+          "dsa_mla_decode_csr_workspace_size")
+    if n.value and (workspace is None or workspace.numel() * workspace.element_size() < n.value):
+        workspace = torch.empty(n.value, dtype=torch.uint8, device=q.device)
+    check(lib.dsa_mla_decode_csr(ctypes.byref(a), _ptr(workspace) if n.value else None, n.value,
+                                 _stream(stream)), "dsa_mla_decode_csr")
+    return out, lse
+
+
 def mla_combine(partial_o: torch.Tensor, partial_lse: torch.Tensor,
                 out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
                 stream=None) -> Tuple[torch.Tensor, torch.Tensor]:

@@ -75,6 +75,7 @@ def _c_layout(struct: str, fields):
 
 
 @pytest.mark.parametrize("cls,name", [(abi.DecodeArgs, "dsa_mla_decode_args"),
+                                      (abi.CsrArgs, "dsa_mla_decode_csr_args"),
                                       (abi.PrefillArgs, "dsa_mla_prefill_args")])
 def test_struct_layout_matches_c(cls, name):
     fields = [f for f, _ in cls._fields_]
@@ -159,6 +160,56 @@ def test_decode_rejects_missing_workspace(lib):
 def test_decode_empty_batch_is_a_no_op(lib):
     a = _decode_args(B=0)
     assert lib.dsa_mla_decode(ctypes.byref(a), None, 0, None) == 0
+
+
+def _csr_args(**kw):
+    a = abi.CsrArgs()
+    a.q, a.kv, a.out, a.lse = 0x1000, 0x2000, 0x3000, 0x4000
+    a.kv_indptr, a.kv_indices = 0x5000, 0x6000
+    a.B, a.s_q, a.H, a.total_tokens = 4, 2, 128, 100000
+    a.stride_q_b, a.stride_q_h = 128 * 576, 576
+    a.stride_o_b, a.stride_o_h = 128 * 512, 512
+    a.kv_format = abi.KV_BF16
+    a.max_kv_len = 3000
+    a.num_splits = 0
+    a.softmax_scale = 0.07
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def _csr_ws(lib, a):
+    n = ctypes.c_size_t(0)
+    rc = lib.dsa_mla_decode_csr_workspace_size(ctypes.byref(a), ctypes.byref(n))
+    return rc, n.value
+
+
+def test_csr_split_plan():
+    lib = abi.load_library()
+    # 3000 rows per batch exceed one workgroup's 2048: at least two splits
+    rc, ws = _csr_ws(lib, _csr_args())
+    assert rc == 0 and ws >= 2 * 4 * 2 * 128 * 513 * 4
+    rc, ws1 = _csr_ws(lib, _csr_args(max_kv_len=2048, B=512, s_q=1))
+    assert rc == 0 and ws1 == 0
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(H=64), -3), (dict(B=-1), -2), (dict(s_q=0), -2), (dict(max_kv_len=-1), -2),
+    (dict(total_tokens=-1), -2), (dict(kv_format=9), -4), (dict(num_splits=65), -6),
+    (dict(max_kv_len=4096, num_splits=1), -6), (dict(max_kv_len=200000), -3),
+    (dict(q=None), -1), (dict(kv=None), -1), (dict(kv_indptr=None), -1), (dict(kv_indices=None), -1),
+    (dict(out=None), -1), (dict(stride_q_h=577), -7), (dict(stride_o_b=-512), -7),
+    (dict(q=0x1004), -7),
+])
+def test_csr_rejects_bad_arguments(lib, kw, code):
+    a = _csr_args(**kw)
+    assert lib.dsa_mla_decode_csr(ctypes.byref(a), None, 0, None) == code
+    assert _csr_ws(lib, a)[0] == code
+
+
+def test_csr_missing_workspace_and_empty_batch(lib):
+    assert lib.dsa_mla_decode_csr(ctypes.byref(_csr_args()), None, 0, None) == -5
+    assert lib.dsa_mla_decode_csr(ctypes.byref(_csr_args(B=0)), None, 0, None) == 0
 
 
 def _prefill_args(**kw):

@@ -1,0 +1,125 @@
+"""GPU parity of the CSR decode entry (dsa_mla_decode_csr) against the CPU oracle.
+
+The CSR form is the reference kernel's own argument set:
+- kv_indptr / kv_indices with page size 1;
+- count-based MTP causality: token t of batch b sees
+  kv_indptr[b+1] - kv_indptr[b] - (s_q - 1 - t) rows,
+  opus_attn/dsa_v32/common/host.cc:482,524-526;
+- an empty range gives O = 0 and LSE = +inf (host.cc:486-489).
+
+The oracle runs the same rows in the top-k form: indices[b, t, :count] are the
+token's CSR rows on a flat cache with seq_len = total_tokens, -1 padded. That
+is the mapping a dsa_v32 harness would use.
+
+Same bar as every parity test: bf16 O max-abs <= 2e-2, LSE within
+1e-3 * (1 + |LSE|) (the reference's rtol = atol = 1e-3 check), and index
+handling exact.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _cases import D_QK, SM_SCALE, assert_parity, bf16_rows, fp8_rows
+from opfoundry_amd import dsa
+
+pytestmark = pytest.mark.gpu
+H = 128
+
+
+def t16(a: np.ndarray, dev) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def csr_case(seed, lens, s_q, total_tokens, fp8=False, bad_rows=0):
+    rng = np.random.default_rng(seed)
+    B = len(lens)
+    kv = fp8_rows(rng, total_tokens) if fp8 else bf16_rows(rng, total_tokens)
+    indptr = np.zeros(B + 1, np.int32)
+    indptr[1:] = np.cumsum(lens)
+    indices = np.concatenate([rng.integers(0, total_tokens, n).astype(np.int32) for n in lens]
+                             + [np.zeros(0, np.int32)])
+    if bad_rows:
+        # rows outside the cache are skipped by the kernel and invalid for the oracle
+        pos = rng.choice(indices.size, bad_rows, replace=False)
+        indices[pos] = np.where(rng.random(bad_rows) < 0.5, -1 - pos, total_tokens + pos).astype(np.int32)
+    q = oracle.normal_bf16(rng, (B * s_q, H, D_QK))
+    return q, kv, indptr, indices
+
+
+def oracle_csr(q, kv, indptr, indices, s_q):
+    """The oracle on the top-k form of the same CSR lists."""
+    B = indptr.size - 1
+    maxc = max(int(indptr[b + 1] - indptr[b]) for b in range(B)) if B else 0
+    idx = np.full((B, s_q, max(maxc, 1)), -1, np.int32)
+    for b in range(B):
+        for t in range(s_q):
+            n = int(indptr[b + 1] - indptr[b]) - (s_q - 1 - t)
+            if n > 0:
+                idx[b, t, :n] = indices[indptr[b]:indptr[b] + n]
+    total = kv.shape[0]
+    sl = np.full(B, total, np.int32)
+    o, lse = oracle.mla_decode(q.reshape(B, s_q, H, D_QK), kv, idx, sl, SM_SCALE)
+    return o.reshape(B * s_q, H, -1), lse.reshape(B * s_q, H)
+
+
+def run_csr(q, kv, indptr, indices, s_q, dev, num_splits=0):
+    kvt = t16(kv, dev) if kv.dtype == np.uint16 else torch.from_numpy(kv).to(dev)
+    out, lse = dsa.mla_decode_csr(t16(q, dev), kvt, torch.from_numpy(indptr).to(dev),
+                                  torch.from_numpy(indices).to(dev), SM_SCALE, s_q=s_q,
+                                  num_splits=num_splits)
+    torch.cuda.synchronize()
+    return bits(out), lse.cpu().numpy()
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_csr_varlen_mtp(dev, fp8):
+    """Varlen lists (one longer than a workgroup's 2048 rows, one empty for token 0
+    under MTP), s_q = 2, and rows outside the cache mixed in."""
+    lens = [700, 3000, 1, 0, 2048]
+    print(f"[case] csr varlen mtp fp8={fp8} lens={lens}", flush=True)
+    q, kv, indptr, indices = csr_case(21 + fp8, lens, 2, 6000, fp8=fp8, bad_rows=40)
+    o_ref, l_ref = oracle_csr(q, kv, indptr, indices, 2)
+    o, l = run_csr(q, kv, indptr, indices, 2, dev)
+    e = assert_parity(o, l, o_ref, l_ref, f"csr varlen mtp fp8={fp8}")
+    print(f"[case] max|dO|={e[0]:.3e} max rel dLSE={e[1]:.3e}", flush=True)
+    # batch 3 has no rows at all; batch 2 has one row, which token 0 of the MTP pair does not see
+    assert np.isinf(l[3 * 2:3 * 2 + 2]).all() and np.isinf(l[2 * 2]).all()
+    assert (o[3 * 2:3 * 2 + 2] == 0).all()
+
+
+def test_csr_reference_shape_c1(dev):
+    """BASELINE config 1 in the reference harness's own form: 2 batches of 1792 compacted
+    rows (kv_indptr = [0, 1792, 3584]), s_q = 1."""
+    print("[case] csr C1 reference shape", flush=True)
+    q, kv, indptr, indices = csr_case(2026, [1792, 1792], 1, 16384)
+    o_ref, l_ref = oracle_csr(q, kv, indptr, indices, 1)
+    for ns in (0, 1, 4):
+        o, l = run_csr(q, kv, indptr, indices, 1, dev, num_splits=ns)
+        e = assert_parity(o, l, o_ref, l_ref, f"csr C1 splits={ns}")
+        print(f"[case] splits={ns}: max|dO|={e[0]:.3e} max rel dLSE={e[1]:.3e}", flush=True)
+
+
+def test_csr_matches_topk_entry_bitwise(dev):
+    """The CSR entry and the top-k entry run the same kernel on the same rows: the outputs
+    are identical bit for bit."""
+    lens = [1500, 900]
+    q, kv, indptr, indices = csr_case(33, lens, 1, 4096)
+    o_csr, l_csr = run_csr(q, kv, indptr, indices, 1, dev, num_splits=1)
+    B = len(lens)
+    idx = np.full((B, 1, max(lens)), -1, np.int32)
+    for b in range(B):
+        idx[b, 0, :lens[b]] = indices[indptr[b]:indptr[b + 1]]
+    out, lse = dsa.mla_decode(t16(q, dev).view(B, 1, H, D_QK), t16(kv, dev),
+                              torch.from_numpy(idx).to(dev), SM_SCALE,
+                              seq_lens=torch.full((B,), kv.shape[0], dtype=torch.int32, device=dev),
+                              num_splits=1)
+    torch.cuda.synchronize()
+    assert (bits(out).reshape(o_csr.shape) == o_csr).all()
+    assert np.array_equal(lse.cpu().numpy().reshape(l_csr.shape), l_csr)

@@ -2,8 +2,8 @@
 
 The HIP path runs on the exact shapes bench.py measures (configs 2-5). The CPU
 oracle then checks a spread sample of query tokens, with the same bar as every
-other parity test: bf16 O max-abs <= 2e-2 on every element and LSE relative
-error <= 1e-3. The sample is kept small so the oracle finishes in seconds.
+other parity test: bf16 O max-abs <= 2e-2 on every element and LSE within
+1e-3 * (1 + |LSE|). The sample is kept small so the oracle finishes in seconds.
 
 Size-independent properties cover every output:
 - all outputs are finite wherever a query has valid indices;
