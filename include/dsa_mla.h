@@ -55,10 +55,12 @@ extern "C" {
 #define DSA_MLA_FP8_ROW_BYTES 656
 #define DSA_MLA_BF16_ROW_BYTES 1152
 #define DSA_MLA_MAX_SPLITS 64
+#define DSA_MLA_D_V4 512       /* V4 prefill head dim: K = V = a 512-value row */
 
 typedef enum {
     DSA_KV_BF16 = 0,
-    DSA_KV_FP8_656 = 1
+    DSA_KV_FP8_656 = 1,
+    DSA_KV_BF16_D512 = 2       /* 512 x bf16 rows (V4 prefill only) */
 } dsa_kv_format;
 
 enum {
@@ -223,6 +225,44 @@ typedef struct {
 int dsa_mla_prefill_workspace_size(const dsa_mla_prefill_args* args, size_t* bytes);
 int dsa_mla_prefill(const dsa_mla_prefill_args* args, void* workspace, size_t workspace_bytes,
                     void* stream);
+
+/*
+ * DeepSeek-V4 sparse MLA prefill: the argument set of opus_mla_v4_prefill_kargs
+ * (opus_attn/dsa_v4/common/mla_v4_kargs.h:10-29), replacing
+ * mla_v4_prefill_launch (opus_attn/dsa_v4/common/mla_v4_host.cc:28-47).
+ * Head dim D = 512: K and V are the same 512-value bf16 row.  Query i, head h:
+ *   rows = unified_kv[kv_indices_prefix[kv_indptr_prefix[i] .. kv_indptr_prefix[i+1])]
+ *        followed by kv[kv_indices_extend[kv_indptr_extend[i] .. kv_indptr_extend[i+1])]
+ *   s_p  = (q[i,h] . row_p) * softmax_scale
+ *   P    = exp(s) / (sum exp(s) + exp(attn_sink[h]))   (no sink term when attn_sink is NULL)
+ *   O    = P . rows, bf16 (mla_v4_host.cc:455-480)
+ * q and out share the strides stride_qo_{n,h} (elements); cache rows are
+ * stride_kv_page elements apart.  A row outside its pool is skipped; a query
+ * with no rows gets O = 0 (and LSE = +inf).  lse (an addition to the
+ * reference, may be NULL) is the natural log of the denominator, sink
+ * included.  max_rows bounds the prefix + extend rows of any query and must be
+ * <= 2048; H must be 128.
+ */
+typedef struct {
+    const void* q;
+    const void* unified_kv;
+    const void* kv;
+    const float* attn_sink;
+    void* out;
+    float* lse;
+    const int32_t* kv_indptr_prefix;
+    const int32_t* kv_indices_prefix;
+    const int32_t* kv_indptr_extend;
+    const int32_t* kv_indices_extend;
+    int32_t N, H, D;
+    int32_t total_pages, total_tokens;
+    int32_t stride_qo_n, stride_qo_h;
+    int32_t stride_kv_page;
+    int32_t max_rows;
+    float softmax_scale;
+} dsa_mla_prefill_v4_args;
+
+int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* args, void* stream);
 
 /*
  * fp8 cache writer: quantise n_rows bf16 latent rows (576 values, row stride

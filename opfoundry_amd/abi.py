@@ -18,6 +18,8 @@ MAX_SPLITS = 64
 
 KV_BF16 = 0
 KV_FP8_656 = 1
+KV_BF16_D512 = 2
+D_V4 = 512
 
 DSA_OK = 0
 ERRORS = {
@@ -41,12 +43,13 @@ EXPORTED_SYMBOLS = (
     "dsa_mla_combine",
     "dsa_mla_prefill_workspace_size",
     "dsa_mla_prefill",
+    "dsa_mla_prefill_v4",
     "dsa_kv_quantize_fp8",
     "dsa_mla_strerror",
     "dsa_mla_abi_version",
 )
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -97,6 +100,19 @@ class PrefillArgs(ctypes.Structure):
     ]
 
 
+class PrefillV4Args(ctypes.Structure):
+    """dsa_mla_prefill_v4_args (include/dsa_mla.h): the reference's opus_mla_v4_prefill_kargs."""
+
+    _fields_ = [
+        ("q", _vp), ("unified_kv", _vp), ("kv", _vp), ("attn_sink", _vp), ("out", _vp), ("lse", _vp),
+        ("kv_indptr_prefix", _vp), ("kv_indices_prefix", _vp),
+        ("kv_indptr_extend", _vp), ("kv_indices_extend", _vp),
+        ("N", _i32), ("H", _i32), ("D", _i32), ("total_pages", _i32), ("total_tokens", _i32),
+        ("stride_qo_n", _i32), ("stride_qo_h", _i32), ("stride_kv_page", _i32), ("max_rows", _i32),
+        ("softmax_scale", ctypes.c_float),
+    ]
+
+
 class DsaError(RuntimeError):
     def __init__(self, code: int, where: str):
         self.code = code
@@ -126,6 +142,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.dsa_mla_combine.argtypes = [_vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _vp]
     lib.dsa_mla_prefill_workspace_size.argtypes = [ctypes.POINTER(PrefillArgs), sz]
     lib.dsa_mla_prefill.argtypes = [ctypes.POINTER(PrefillArgs), _vp, ctypes.c_size_t, _vp]
+    lib.dsa_mla_prefill_v4.argtypes = [ctypes.POINTER(PrefillV4Args), _vp]
     lib.dsa_kv_quantize_fp8.argtypes = [_vp, _i64, _i64, _vp, _i64, _vp, _vp]
     lib.dsa_mla_strerror.argtypes = [ctypes.c_int]
     lib.dsa_mla_strerror.restype = ctypes.c_char_p

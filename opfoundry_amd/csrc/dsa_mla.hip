@@ -65,6 +65,7 @@ constexpr int RAW_STRIDE = FP8_LOADS * 1024;         // raw slot padded to whole
 constexpr int FP8_LPW = (FP8_LOADS + NWAVE - 1) / NWAVE;  // loads of wave 0 (6); the others 5
 constexpr int BF16_LPW = TILE / NWAVE + 1;           // 8 NoPE rows + one 8-row RoPE block
 constexpr int FP8_SCALE_OFF = D_NOPE;                // 4 fp32 scales
+constexpr int32_t POOL2 = 1 << 30;                   // row-list tag: a row of the second pool (V4 extend)
 constexpr int FP8_ROPE_OFF = D_NOPE + 16;            // 64 bf16 RoPE values
 
 __device__ __forceinline__ int nope_sw(int r) { return (r >> 2) & 3; }
@@ -75,8 +76,10 @@ __device__ __forceinline__ int rope_sw(int r) { return (r >> 1) & 7; }
 template <int FMT>
 struct Lay {
     static constexpr bool FP8 = FMT == DSA_KV_FP8_656;
+    static constexpr bool D512 = FMT == DSA_KV_BF16_D512;  // 512-value rows: K = V = the whole row
     static constexpr int RING_BYTES = FP8 ? 3 * RAW_STRIDE : TILE_BYTES;
-    static constexpr int LPW = FP8 ? FP8_LPW : BF16_LPW;  // max DMA loads per wave per tile
+    static constexpr int LPW = FP8 ? FP8_LPW : (D512 ? TILE / NWAVE : BF16_LPW);  // max DMA loads per wave per tile
+    static constexpr int KS = D512 ? KS_NOPE : KS_ALL;    // 16-deep k-steps of QK^T
     // p = exp2(s - m_ref) may grow to 2^TAU over the reference before a
     // restart: fp16 P (fp8 cache) is finite below 2^16, bf16 P below 2^128.
     static constexpr float TAU = FP8 ? 15.0f : 100.0f;
@@ -177,6 +180,16 @@ struct FwdParams {
     int64_t idx_sb, idx_st;
     const int32_t* kv_indptr;    // CSR form (NULL: top-k form): rows kv_indices[kv_indptr[b] + k]
     const int32_t* kv_indices;
+    // V4 prefill form (ind_pre != NULL): query b attends idx_pre[ind_pre[b] ..
+    // ind_pre[b+1]) of kv, then idx_ext[ind_ext[b] .. ind_ext[b+1]) of kv2
+    const int32_t* ind_pre;
+    const int32_t* idx_pre;
+    const int32_t* ind_ext;
+    const int32_t* idx_ext;
+    const unsigned char* kv2;    // second row pool (V4 extend rows)
+    int64_t kv2_rows;
+    int64_t row_bytes;           // bytes between cache rows (512-value rows)
+    const float* attn_sink;      // per-head sink in the softmax denominator, or NULL
     __bf16* out;
     int64_t o_sb, o_st, o_sh;
     float* lse;
@@ -279,11 +292,11 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 
     // ---- 0. Q fragments (B operand of S^T = K Q^T): lane -> head r32, k-chunk hi ----
     // Issued first so their latency overlaps the index resolution below.
-    u32x4 qf[KS_ALL];
+    u32x4 qf[L::KS];
     {
         const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head * p.q_sh + 8 * hi;
 #pragma unroll
-        for (int ks = 0; ks < KS_ALL; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * ks);
+        for (int ks = 0; ks < L::KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * ks);
     }
 
     // ---- 1. resolve this split's index chunk into a compacted row list ----
@@ -297,7 +310,17 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     int k1;
     int64_t jmax = 0;
     const int32_t* idx;
-    if (p.kv_indptr) {
+    int64_t v4_np = 0, v4_eb = 0;
+    if (L::D512 && p.ind_pre) {
+        // V4: prefix rows of kv, then extend rows of kv2 (tagged with POOL2);
+        // a decreasing indptr pair counts as an empty range
+        const int64_t pb = p.ind_pre[b];
+        v4_np = max((int64_t)p.ind_pre[b + 1] - pb, (int64_t)0);
+        v4_eb = p.ind_ext[b];
+        const int64_t ne = max((int64_t)p.ind_ext[b + 1] - v4_eb, (int64_t)0);
+        k1 = (int)min((int64_t)k0 + p.chunk, v4_np + ne);
+        idx = p.idx_pre + pb;
+    } else if (p.kv_indptr) {
         const int64_t kb = p.kv_indptr[b];
         const int64_t count = (int64_t)p.kv_indptr[b + 1] - kb - (p.s_q - 1 - t);
         k1 = (int)min((int64_t)k0 + p.chunk, count);
@@ -319,12 +342,20 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 #pragma unroll
         for (int e = 0; e < PER_T; ++e) {
             const int k = k0 + tid * PER_T + e;
-            jv[e] = k < k1 ? idx[k] : -1;
+            if (L::D512 && p.ind_pre && k < k1 && k >= v4_np) {
+                const int32_t j = p.idx_ext[v4_eb + (k - v4_np)];
+                jv[e] = j >= 0 && (int64_t)j < p.kv2_rows ? (j | POOL2) : -1;
+            } else {
+                jv[e] = k < k1 ? idx[k] : -1;
+            }
         }
 #pragma unroll
         for (int e = 0; e < PER_T; ++e) {
-            rows_local[e] = p.kv_indptr ? (jv[e] >= 0 && (int64_t)jv[e] < p.kv_total_rows ? jv[e] : -1)
-                                        : (int32_t)resolve_row(p, b, jmax, jv[e]);
+            if (L::D512 && p.ind_pre)   // extend ids were checked above; prefix ids against kv
+                rows_local[e] = (jv[e] & POOL2) ? jv[e] : (jv[e] >= 0 && (int64_t)jv[e] < p.kv_total_rows ? jv[e] : -1);
+            else
+                rows_local[e] = p.kv_indptr ? (jv[e] >= 0 && (int64_t)jv[e] < p.kv_total_rows ? jv[e] : -1)
+                                            : (int32_t)resolve_row(p, b, jmax, jv[e]);
             cnt += rows_local[e] >= 0 ? 1 : 0;
         }
     }
@@ -398,9 +429,16 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             const lds_ptr tb = slot_buf(slot);
             if (i < 8) {
                 const int r = 8 * wave + i;
-                const unsigned char* src = p.kv + (int64_t)g.r[i] * BF16_ROW + 16 * (ln ^ nope_sw(r));
+                const unsigned char* src;
+                if constexpr (L::D512) {
+                    const int32_t id = g.r[i];   // wave-uniform: the pool choice is scalar
+                    const unsigned char* base = (id & POOL2) ? p.kv2 : p.kv;
+                    src = base + (int64_t)(id & (POOL2 - 1)) * p.row_bytes + 16 * (ln ^ nope_sw(r));
+                } else {
+                    src = p.kv + (int64_t)g.r[i] * BF16_ROW + 16 * (ln ^ nope_sw(r));
+                }
                 lds_dma16(src, tb + r * NOPE_STRIDE);
-            } else {
+            } else if constexpr (!L::D512) {
                 const int r = 8 * wave + (ln >> 3);
                 const unsigned char* src =
                     p.kv + (int64_t)g.rope * BF16_ROW + 2 * D_NOPE + 16 * ((ln & 7) ^ rope_sw(r));
@@ -570,12 +608,12 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         // issues at about 60 % of the MFMA rate, two interleaved chains at full rate
         f32x16 sacc2[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-        for (int ks = 0; ks < KS_ALL; ++ks) {
+        for (int ks = 0; ks < L::KS; ++ks) {
             __builtin_amdgcn_sched_barrier(0);
             f32x16& acc = sacc2[ks & 1];
             if (FP8 && ks < KS_NOPE) acc = mfma_f16(kb[ks % KPF], qf[ks], acc);
             else acc = mfma_bf16(kb[ks % KPF], qf[ks], acc);
-            if (ks + KPF < KS_ALL) kb[ks % KPF] = lds_ld<u32x4>(k_addr(ks + KPF));
+            if (ks + KPF < L::KS) kb[ks % KPF] = lds_ld<u32x4>(k_addr(ks + KPF));
         }
         __builtin_amdgcn_sched_barrier(0);
         f32x16 sacc = sacc2[0] + sacc2[1];
@@ -611,10 +649,14 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             // rounded - the order the reference uses
             // (opus_attn/dsa_v32/common/host.cc:448-451); with few rows the
             // outputs are large and a different rounding order would show.
+            // (an attention sink joins the sum: mla_v4_host.cc:469-472)
             float lt = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) lt += __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], c_s, -m_ref));
-            m_ref += __builtin_amdgcn_logf(lt + __shfl_xor(lt, 32, 64));
+            lt += __shfl_xor(lt, 32, 64);
+            if constexpr (L::D512)
+                if (p.attn_sink) lt += __builtin_amdgcn_exp2f(__builtin_fmaf(p.attn_sink[head], LOG2E, -m_ref));
+            m_ref += __builtin_amdgcn_logf(lt);
         }
         {
             float e[16];
@@ -743,8 +785,13 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // ---- epilogue ----
     // Wave w holds O for dims 128w..128w+127 of all heads; the softmax sums
     // and references are per head, owned by the head's QK wave: exchange them.
-    const float l = l_lane + __shfl_xor(l_lane, 32, 64);
-    const bool has = l > 0.0f;
+    const float l_rows = l_lane + __shfl_xor(l_lane, 32, 64);
+    const bool has = l_rows > 0.0f;
+    // the softmax denominator: the rows' sum plus an attention sink, exp(sink - m)
+    // (mla_v4_host.cc:469-472; LSE then covers the sink as well)
+    float l = l_rows;
+    if constexpr (L::D512)
+        if (p.attn_sink) l += __builtin_amdgcn_exp2f(__builtin_fmaf(p.attn_sink[head], LOG2E, -m_ref));
     const int64_t qrow = (int64_t)b * p.s_q + t;
     LDS_AS float* const s_l = (LDS_AS float*)PX;      // P buffer is free now
     if (hi == 0) s_l[head] = has ? (ntiles == 1 ? 1.0f : 1.0f / l) : 0.0f;   // one tile: P is normalised
@@ -952,7 +999,8 @@ size_t decode_ws_bytes(const dsa_mla_decode_args* a, int ns) {
 int launch_fwd(const FwdParams& fp, int fmt, int B, int s_q, int ns, hipStream_t st) {
     dim3 grid(B, s_q, ns), block(NTHR);
     if (fmt == DSA_KV_BF16) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_BF16>, grid, block, 0, st, fp);
-    else hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_FP8_656>, grid, block, 0, st, fp);
+    else if (fmt == DSA_KV_FP8_656) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_FP8_656>, grid, block, 0, st, fp);
+    else hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_BF16_D512>, grid, block, 0, st, fp);
     return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_HIP;
 }
 
@@ -996,7 +1044,7 @@ size_t csr_ws_bytes(const dsa_mla_decode_csr_args* a, int ns) {
 
 extern "C" {
 
-int dsa_mla_abi_version(void) { return 2; }
+int dsa_mla_abi_version(void) { return 3; }
 
 const char* dsa_mla_strerror(int code) {
     switch (code) {
@@ -1165,6 +1213,40 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* a, void* ws, size_t ws_bytes, vo
     return launch_fwd(fp, a->kv_format, a->N, 1, 1, (hipStream_t)stream);
 }
 
+int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* a, void* stream) {
+    if (!a) return DSA_ERR_NULL_POINTER;
+    if (a->N < 0 || a->total_pages < 0 || a->total_tokens < 0 || a->max_rows < 0) return DSA_ERR_BAD_SHAPE;
+    if (a->H != HEADS || a->D != DSA_MLA_D_V4 || a->max_rows > MAX_CHUNK) return DSA_ERR_UNSUPPORTED;
+    if (a->N == 0) return DSA_OK;
+    if (!a->q || !a->out || !a->kv_indptr_prefix || !a->kv_indices_prefix || !a->kv_indptr_extend ||
+        !a->kv_indices_extend)
+        return DSA_ERR_NULL_POINTER;
+    if ((a->total_pages > 0 && !a->unified_kv) || (a->total_tokens > 0 && !a->kv)) return DSA_ERR_NULL_POINTER;
+    if (a->stride_qo_n < 0 || a->stride_qo_h < 0 || (a->stride_qo_n % 8) || (a->stride_qo_h % 8) ||
+        a->stride_kv_page < DSA_MLA_D_V4 || (a->stride_kv_page % 8))
+        return DSA_ERR_BAD_STRIDE;
+    if (((uintptr_t)a->q & 15) || ((uintptr_t)a->unified_kv & 15) || ((uintptr_t)a->kv & 15) ||
+        ((uintptr_t)a->out & 7))
+        return DSA_ERR_BAD_STRIDE;
+    FwdParams fp{};
+    fp.q = (const __bf16*)a->q;
+    fp.q_sb = a->stride_qo_n; fp.q_st = 0; fp.q_sh = a->stride_qo_h;
+    fp.kv = (const unsigned char*)a->unified_kv;
+    fp.kv_total_rows = a->total_pages;
+    fp.kv2 = (const unsigned char*)a->kv;
+    fp.kv2_rows = a->total_tokens;
+    fp.row_bytes = (int64_t)a->stride_kv_page * 2;
+    fp.block_size = 1;
+    fp.ind_pre = a->kv_indptr_prefix; fp.idx_pre = a->kv_indices_prefix;
+    fp.ind_ext = a->kv_indptr_extend; fp.idx_ext = a->kv_indices_extend;
+    fp.attn_sink = a->attn_sink;
+    fp.out = (__bf16*)a->out;
+    fp.o_sb = a->stride_qo_n; fp.o_st = 0; fp.o_sh = a->stride_qo_h;
+    fp.lse = a->lse;
+    fp.B = a->N; fp.s_q = 1; fp.topk = a->max_rows; fp.chunk = a->max_rows;
+    fp.scale_log2 = a->softmax_scale * LOG2E;
+    return launch_fwd(fp, DSA_KV_BF16_D512, a->N, 1, 1, (hipStream_t)stream);
+}
 int dsa_kv_quantize_fp8(const void* src, int64_t src_stride, int64_t n_rows, void* dst, int64_t dst_total,
                         const int64_t* dst_rows, void* stream) {
     if (n_rows < 0 || dst_total < 0) return DSA_ERR_BAD_SHAPE;

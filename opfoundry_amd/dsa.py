@@ -265,6 +265,54 @@ def mla_prefill(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor, sm_sca
     return out, lse
 
 
+def mla_prefill_v4(q: torch.Tensor, unified_kv: torch.Tensor, kv: torch.Tensor,
+                   attn_sink: Optional[torch.Tensor], kv_indptr_prefix: torch.Tensor,
+                   kv_indices_prefix: torch.Tensor, kv_indptr_extend: torch.Tensor,
+                   kv_indices_extend: torch.Tensor, softmax_scale: float,
+                   out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None, *,
+                   max_rows: Optional[int] = None, stream=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """DeepSeek-V4 sparse prefill (opus_mla_v4_prefill_kargs form): q [N, H, 512] bf16, prefix
+    rows from unified_kv [total_pages, 512], extend rows from kv [total_tokens, 512], per-head
+    attn_sink fp32 [H] in the softmax denominator (or None); returns (out [N, H, 512], lse [N, H])."""
+    _need(q, torch.bfloat16, "q")
+    for t, n in ((unified_kv, "unified_kv"), (kv, "kv")):
+        _need(t, torch.bfloat16, n)
+        if t.shape[-1] != abi.D_V4 or t.stride(-1) != 1:
+            raise ValueError(f"{n} must be [rows, 512] bf16 with a dense last dim")
+    for t, n in ((kv_indptr_prefix, "kv_indptr_prefix"), (kv_indices_prefix, "kv_indices_prefix"),
+                 (kv_indptr_extend, "kv_indptr_extend"), (kv_indices_extend, "kv_indices_extend")):
+        _need(t, torch.int32, n)
+    if attn_sink is not None:
+        _need(attn_sink, torch.float32, "attn_sink")
+    N, H, D = q.shape
+    if D != abi.D_V4 or q.stride(2) != 1:
+        raise ValueError("q must be [N, H, 512] with a dense last dim")
+    if out is None:
+        out = torch.empty_like(q)
+    if out.stride() != q.stride():
+        raise ValueError("out must have q's strides (the reference shares stride_qo_n / stride_qo_h)")
+    if lse is None:
+        lse = torch.empty((N, H), dtype=torch.float32, device=q.device)
+    if max_rows is None:
+        max_rows = int(((kv_indptr_prefix[1:] - kv_indptr_prefix[:-1]) +
+                        (kv_indptr_extend[1:] - kv_indptr_extend[:-1])).max()) if N else 0
+    a = abi.PrefillV4Args()
+    a.q, a.unified_kv, a.kv, a.attn_sink = _ptr(q), _ptr(unified_kv), _ptr(kv), _ptr(attn_sink)
+    a.out, a.lse = _ptr(out), _ptr(lse)
+    a.kv_indptr_prefix, a.kv_indices_prefix = _ptr(kv_indptr_prefix), _ptr(kv_indices_prefix)
+    a.kv_indptr_extend, a.kv_indices_extend = _ptr(kv_indptr_extend), _ptr(kv_indices_extend)
+    a.N, a.H, a.D = N, H, D
+    a.total_pages, a.total_tokens = unified_kv.shape[0], kv.shape[0]
+    a.stride_qo_n, a.stride_qo_h = q.stride(0), q.stride(1)
+    a.stride_kv_page = unified_kv.stride(0)
+    if kv.stride(0) != unified_kv.stride(0):
+        raise ValueError("unified_kv and kv must share the row stride (stride_kv_page)")
+    a.max_rows = int(max_rows)
+    a.softmax_scale = float(softmax_scale)
+    check(load_library().dsa_mla_prefill_v4(ctypes.byref(a), _stream(stream)), "dsa_mla_prefill_v4")
+    return out, lse
+
+
 def quantize_kv_fp8(src: torch.Tensor, dst: Optional[torch.Tensor] = None,
                     dst_rows: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
     """Write bf16 latent rows [n, 576] into 656-byte fp8 cache rows (uint8 [rows, 656])."""

@@ -20,7 +20,7 @@ import subprocess
 
 import numpy as np
 
-from opfoundry_amd.abi import D_QK, D_VO, DecodeArgs, KV_BF16, KV_FP8_656, PrefillArgs
+from opfoundry_amd.abi import D_QK, D_V4, D_VO, DecodeArgs, KV_BF16, KV_FP8_656, PrefillArgs, PrefillV4Args
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "_build", "libdsa_oracle.so")
@@ -56,6 +56,7 @@ def lib() -> ctypes.CDLL:
         L.oracle_mla_combine.argtypes = [vp, vp, i32, i64, i32, vp, vp]
         L.oracle_mla_combine.restype = None
         L.oracle_mla_prefill.argtypes = [ctypes.POINTER(PrefillArgs), ctypes.c_int]
+        L.oracle_mla_prefill_v4.argtypes = [ctypes.POINTER(PrefillV4Args), ctypes.c_int]
         L.oracle_num_threads.argtypes = [ctypes.c_int]
         _LIB = L
     return _LIB
@@ -190,6 +191,35 @@ def mla_combine(part_o: np.ndarray, part_lse: np.ndarray):
     out = np.zeros((rows, H, D_VO), np.uint16)
     lse = np.zeros((rows, H), np.float32)
     lib().oracle_mla_combine(_p(po), _p(pl), S, rows, H, _p(out), _p(lse))
+    return out, lse
+
+
+def mla_prefill_v4(q, unified_kv, kv, attn_sink, indptr_prefix, indices_prefix, indptr_extend,
+                   indices_extend, softmax_scale, *, num_threads=0):
+    """Host oracle of dsa_mla_prefill_v4: q uint16 [N,H,512]; unified_kv / kv uint16 [rows,512];
+    attn_sink float32 [H] or None; CSR lists int32.  Returns (O uint16 [N,H,512], LSE f32)."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    ukv = np.ascontiguousarray(unified_kv, dtype=np.uint16).reshape(-1, D_V4)
+    xkv = np.ascontiguousarray(kv, dtype=np.uint16).reshape(-1, D_V4)
+    sink = None if attn_sink is None else np.ascontiguousarray(attn_sink, dtype=np.float32)
+    ipp, idp = (np.ascontiguousarray(x, dtype=np.int32) for x in (indptr_prefix, indices_prefix))
+    ipe, ide = (np.ascontiguousarray(x, dtype=np.int32) for x in (indptr_extend, indices_extend))
+    N, H, _ = q.shape
+    out = np.zeros((N, H, D_V4), np.uint16)
+    lse = np.zeros((N, H), np.float32)
+    max_rows = int(max((ipp[1:] - ipp[:-1]).max(initial=0) + (ipe[1:] - ipe[:-1]).max(initial=0), 1))
+    a = PrefillV4Args()
+    a.q, a.unified_kv, a.kv, a.attn_sink, a.out, a.lse = _p(q), _p(ukv), _p(xkv), _p(sink), _p(out), _p(lse)
+    a.kv_indptr_prefix, a.kv_indices_prefix = _p(ipp), _p(idp)
+    a.kv_indptr_extend, a.kv_indices_extend = _p(ipe), _p(ide)
+    a.N, a.H, a.D = N, H, D_V4
+    a.total_pages, a.total_tokens = ukv.shape[0], xkv.shape[0]
+    a.stride_qo_n, a.stride_qo_h = H * D_V4, D_V4
+    a.stride_kv_page = D_V4
+    a.max_rows = max_rows
+    a.softmax_scale = float(softmax_scale)
+    rc = lib().oracle_mla_prefill_v4(ctypes.byref(a), num_threads)
+    assert rc == 0
     return out, lse
 
 

@@ -18,6 +18,8 @@
  *   - per-query prefill reference . opus_attn/dsa_v4/common/mla_v4_host.cc:482-532
  *                                   (no sink: sink = -inf reduces :469,:472 to
  *                                   the decode core)
+ *   - V4 prefill (prefix + extend
+ *     pools, attention sink, D=512) opus_attn/dsa_v4/common/mla_v4_host.cc:455-532
  *   - split combine ............... opus_attn/dsa_v32/common/mla_reduce.hpp:6-156
  *   - threading ................... opus_attn/dsa_v32/common/parallel.h:11-57
  * generalised to the top-k index form (-1 padding, seq_len and causal bounds,
@@ -390,6 +392,86 @@ static void prefill_task(void* vctx, int64_t i, float* scratch) {
         uint16_t* o = (uint16_t*)a->out + i * a->o_stride_n + h * a->o_stride_h;
         attention_core(q, kv, n, a->sm_scale, scores, o, NULL, a->lse ? a->lse + i * a->H + h : NULL);
     }
+}
+
+/* ------------------------------------------------------- V4 prefill */
+
+/*
+ * mla_v4_attention_compute (opus_attn/dsa_v4/common/mla_v4_host.cc:455-480)
+ * with softmax_scale as a parameter (:461 hard-codes 1/sqrt(D)): scores in
+ * fp32, max over the scores and the sink, denominator sum exp(s - max) +
+ * exp(sink - max), P rounded to bf16 after normalisation, O = P . rows
+ * (V = the whole 512-value row) cast to bf16.  LSE = max + ln(denominator),
+ * an addition of this build; a query with no rows gets O = 0, LSE = +inf.
+ */
+static void attention_core_v4(const float* q, const float* kv, int n, float scale, float sink,
+                              float* scores, uint16_t* o_bf16, float* lse) {
+    const int D = DSA_MLA_D_V4;
+    if (n <= 0) {
+        for (int d = 0; d < D; ++d) o_bf16[d] = 0;
+        if (lse) *lse = INFINITY;
+        return;
+    }
+    for (int p = 0; p < n; ++p) {
+        const float* k = kv + (size_t)p * D;
+        float dot = 0.0f;
+        for (int d = 0; d < D; ++d) dot += q[d] * k[d];
+        scores[p] = dot * scale;
+    }
+    float mx = sink;
+    for (int p = 0; p < n; ++p) if (scores[p] > mx) mx = scores[p];
+    float sum = 0.0f;
+    for (int p = 0; p < n; ++p) { scores[p] = expf(scores[p] - mx); sum += scores[p]; }
+    sum += expf(sink - mx);
+    if (lse) *lse = logf(sum) + mx;
+    for (int p = 0; p < n; ++p) scores[p] = oracle_bf16_to_f32(oracle_f32_to_bf16(scores[p] / sum));
+    for (int d = 0; d < D; ++d) {
+        float acc = 0.0f;
+        for (int p = 0; p < n; ++p) acc += scores[p] * kv[(size_t)p * D + d];
+        o_bf16[d] = oracle_f32_to_bf16(acc);
+    }
+}
+
+typedef struct {
+    const dsa_mla_prefill_v4_args* a;
+} prefill_v4_ctx;
+
+/* mla_v4_attention_ref (mla_v4_host.cc:482-532): prefix rows, then extend rows. */
+static void prefill_v4_task(void* vctx, int64_t i, float* scratch) {
+    const dsa_mla_prefill_v4_args* a = ((const prefill_v4_ctx*)vctx)->a;
+    const int D = DSA_MLA_D_V4;
+    float* q = scratch;
+    float* scores = q + D;
+    float* kv = scores + a->max_rows;
+    int n = 0;
+    const int32_t pb = a->kv_indptr_prefix[i], pe = a->kv_indptr_prefix[i + 1];
+    const int32_t eb = a->kv_indptr_extend[i], ee = a->kv_indptr_extend[i + 1];
+    for (int pass = 0; pass < 2; ++pass) {
+        const int32_t* ind = pass == 0 ? a->kv_indices_prefix : a->kv_indices_extend;
+        const uint16_t* pool = (const uint16_t*)(pass == 0 ? a->unified_kv : a->kv);
+        const int32_t rows = pass == 0 ? a->total_pages : a->total_tokens;
+        for (int32_t k = pass == 0 ? pb : eb; k < (pass == 0 ? pe : ee) && n < a->max_rows; ++k) {
+            const int32_t j = ind[k];
+            if (j < 0 || j >= rows) continue;   /* a row outside its pool is skipped */
+            const uint16_t* src = pool + (int64_t)j * a->stride_kv_page;
+            for (int d = 0; d < D; ++d) kv[(size_t)n * D + d] = oracle_bf16_to_f32(src[d]);
+            ++n;
+        }
+    }
+    const uint16_t* qb = (const uint16_t*)a->q;
+    for (int h = 0; h < a->H; ++h) {
+        const uint16_t* qs = qb + i * a->stride_qo_n + h * a->stride_qo_h;
+        for (int d = 0; d < D; ++d) q[d] = oracle_bf16_to_f32(qs[d]);
+        uint16_t* o = (uint16_t*)a->out + i * a->stride_qo_n + h * a->stride_qo_h;
+        const float sink = a->attn_sink ? a->attn_sink[h] : -INFINITY;
+        attention_core_v4(q, kv, n, a->softmax_scale, sink, scores, o, a->lse ? a->lse + i * a->H + h : NULL);
+    }
+}
+
+int oracle_mla_prefill_v4(const dsa_mla_prefill_v4_args* a, int nthreads) {
+    prefill_v4_ctx c = {a};
+    const size_t scratch = (size_t)DSA_MLA_D_V4 + a->max_rows + (size_t)a->max_rows * DSA_MLA_D_V4;
+    return run_pool(prefill_v4_task, &c, a->N, scratch, nthreads);
 }
 
 /* mla_v4_host.cc:482-532 for the V3.2 shape without sink, with LSE. */

@@ -76,6 +76,7 @@ def _c_layout(struct: str, fields):
 
 @pytest.mark.parametrize("cls,name", [(abi.DecodeArgs, "dsa_mla_decode_args"),
                                       (abi.CsrArgs, "dsa_mla_decode_csr_args"),
+                                      (abi.PrefillV4Args, "dsa_mla_prefill_v4_args"),
                                       (abi.PrefillArgs, "dsa_mla_prefill_args")])
 def test_struct_layout_matches_c(cls, name):
     fields = [f for f, _ in cls._fields_]
@@ -210,6 +211,38 @@ def test_csr_rejects_bad_arguments(lib, kw, code):
 def test_csr_missing_workspace_and_empty_batch(lib):
     assert lib.dsa_mla_decode_csr(ctypes.byref(_csr_args()), None, 0, None) == -5
     assert lib.dsa_mla_decode_csr(ctypes.byref(_csr_args(B=0)), None, 0, None) == 0
+
+
+def _v4_args(**kw):
+    a = abi.PrefillV4Args()
+    a.q, a.unified_kv, a.kv, a.attn_sink, a.out, a.lse = 0x1000, 0x2000, 0x3000, 0x4000, 0x5000, 0x6000
+    a.kv_indptr_prefix, a.kv_indices_prefix = 0x7000, 0x8000
+    a.kv_indptr_extend, a.kv_indices_extend = 0x9000, 0xA000
+    a.N, a.H, a.D = 64, 128, 512
+    a.total_pages, a.total_tokens = 65536, 4096
+    a.stride_qo_n, a.stride_qo_h = 128 * 512, 512
+    a.stride_kv_page = 512
+    a.max_rows = 1152
+    a.softmax_scale = 0.044
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(H=64), -3), (dict(D=576), -3), (dict(max_rows=2049), -3), (dict(N=-1), -2),
+    (dict(total_pages=-1), -2), (dict(max_rows=-1), -2),
+    (dict(q=None), -1), (dict(out=None), -1), (dict(kv_indptr_prefix=None), -1),
+    (dict(kv_indices_extend=None), -1), (dict(unified_kv=None), -1), (dict(kv=None), -1),
+    (dict(stride_kv_page=500), -7), (dict(stride_kv_page=516), -7), (dict(stride_qo_h=513), -7),
+    (dict(q=0x1008), -7), (dict(out=0x5004), -7),
+])
+def test_prefill_v4_rejects_bad_arguments(lib, kw, code):
+    assert lib.dsa_mla_prefill_v4(ctypes.byref(_v4_args(**kw)), None) == code
+
+
+def test_prefill_v4_empty_is_a_no_op(lib):
+    assert lib.dsa_mla_prefill_v4(ctypes.byref(_v4_args(N=0)), None) == 0
 
 
 def _prefill_args(**kw):
