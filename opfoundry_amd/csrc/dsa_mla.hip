@@ -587,7 +587,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         // Software pipeline pinned with scheduling barriers: the K fragment of
         // k-step ks+KPF is read while MFMA ks runs; the gathers of tile
         // it+NPRE are issued between the MFMAs (one load every 4 k-steps).
-        constexpr int KPF = 4;
+        constexpr int KPF = FP8 ? 4 : 6;     // fp8: register-bound at 4
         auto k_addr = [&](int ks) -> lds_cptr {
             return ks < KS_NOPE ? ((ks & 1) ? k_odd : k_even) + 64 * (ks >> 1)
                                 : k_rope + 16 * ((2 * (ks - KS_NOPE) + lhi) ^ rsw);
