@@ -60,7 +60,8 @@ extern "C" {
 typedef enum {
     DSA_KV_BF16 = 0,
     DSA_KV_FP8_656 = 1,
-    DSA_KV_BF16_D512 = 2       /* 512 x bf16 rows (V4 prefill only) */
+    DSA_KV_BF16_D512 = 2,      /* 512 x bf16 rows (V4 prefill only) */
+    DSA_KV_MXFP8 = 3           /* MXFP8 split streams (dsa_mla_decode_mxfp8 only) */
 } dsa_kv_format;
 
 enum {
@@ -193,6 +194,59 @@ int dsa_mla_decode_csr_workspace_size(const dsa_mla_decode_csr_args* args, size_
 /* Launch the CSR decode (kernel + split combine) on `stream`. */
 int dsa_mla_decode_csr(const dsa_mla_decode_csr_args* args, void* workspace, size_t workspace_bytes,
                        void* stream);
+
+/*
+ * Sparse MLA decode on MXFP8 split streams, CSR form: the argument set of
+ * opus_mla_decode_mxfp8_kargs (opus_attn/dsa_v32/common/defs.h:75-107, minus
+ * the work / plan pointers), the reference's own "-dtype fp8" format
+ * (opus_attn/dsa_v32/common/host.cc:551-697, opus_attn/dsa_v32/README.md:55-57).
+ * It replaces the launch of opus_mla_decode_mxfp8_16mx8_32nx1_kernel
+ * (host.cc:32-37), whose device source the reference does not ship.
+ * Query row i = b * s_q + t, head h:
+ *   q_nope  : fp8 e4m3fn [512] at q_nope + i * stride_q_nope_b + h * stride_q_nope_h
+ *   q_scale : E8M0 [16]   at q_scale + i * stride_q_scale_b + h * stride_q_scale_h
+ *   q_rope  : bf16 [64]   at q_rope + i * stride_q_rope_b + h * stride_q_rope_h
+ * Cache row r (page size 1):
+ *   kv_nope : fp8 e4m3fn [512] at kv_nope + r * stride_kv_nope_page
+ *   kv_scale: E8M0 [16]        at kv_scale + r * stride_kv_scale_page
+ *   kv_rope : bf16 [64]        at kv_rope + r * stride_kv_rope_page
+ * (strides in elements of each stream: bytes for fp8 and E8M0, bf16 elements
+ * for rope and out).  Value of NoPE dim d = float(e4m3(code_d)) *
+ * 2^(scale[d / 32] - 127), RoPE as stored (dequant_mla_row_fp8,
+ * host.cc:418-429); the kernel computes exactly these values.  Index
+ * semantics, out, lse, max_kv_len and num_splits as in dsa_mla_decode_csr.
+ * Alignment: the six stream pointers 16 bytes; fp8 and E8M0 strides
+ * multiples of 16, bf16 strides multiples of 8, out strides of 4.
+ */
+typedef struct {
+    const void* q_nope;
+    const void* q_scale;
+    const void* q_rope;
+    const void* kv_nope;
+    const void* kv_scale;
+    const void* kv_rope;
+    void* out;
+    float* lse;
+    const int32_t* kv_indptr;
+    const int32_t* kv_indices;
+    int32_t B, s_q, H;
+    int32_t total_tokens;
+    int32_t stride_q_nope_b, stride_q_nope_h;
+    int32_t stride_q_scale_b, stride_q_scale_h;
+    int32_t stride_q_rope_b, stride_q_rope_h;
+    int32_t stride_o_b, stride_o_h;
+    int32_t stride_kv_nope_page, stride_kv_scale_page, stride_kv_rope_page;
+    int32_t max_kv_len;
+    int32_t num_splits;          /* 0 = automatic */
+    float softmax_scale;
+} dsa_mla_decode_mxfp8_args;
+
+/* Workspace bytes dsa_mla_decode_mxfp8 needs (0 when unsplit). */
+int dsa_mla_decode_mxfp8_workspace_size(const dsa_mla_decode_mxfp8_args* args, size_t* bytes);
+
+/* Launch the MXFP8 decode (kernel + split combine) on `stream`. */
+int dsa_mla_decode_mxfp8(const dsa_mla_decode_mxfp8_args* args, void* workspace,
+                         size_t workspace_bytes, void* stream);
 
 /*
  * Sparse MLA prefill (per-query top-k over one KV pool).

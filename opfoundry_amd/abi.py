@@ -19,6 +19,7 @@ MAX_SPLITS = 64
 KV_BF16 = 0
 KV_FP8_656 = 1
 KV_BF16_D512 = 2
+KV_MXFP8 = 3
 D_V4 = 512
 
 DSA_OK = 0
@@ -40,6 +41,8 @@ EXPORTED_SYMBOLS = (
     "dsa_mla_decode",
     "dsa_mla_decode_csr_workspace_size",
     "dsa_mla_decode_csr",
+    "dsa_mla_decode_mxfp8_workspace_size",
+    "dsa_mla_decode_mxfp8",
     "dsa_mla_combine",
     "dsa_mla_prefill_workspace_size",
     "dsa_mla_prefill",
@@ -49,7 +52,7 @@ EXPORTED_SYMBOLS = (
     "dsa_mla_abi_version",
 )
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -82,6 +85,25 @@ class CsrArgs(ctypes.Structure):
         ("B", _i32), ("s_q", _i32), ("H", _i32), ("total_tokens", _i32),
         ("stride_q_b", _i32), ("stride_q_h", _i32), ("stride_o_b", _i32), ("stride_o_h", _i32),
         ("kv_format", _i32), ("max_kv_len", _i32), ("num_splits", _i32),
+        ("softmax_scale", ctypes.c_float),
+    ]
+
+
+class MxArgs(ctypes.Structure):
+    """dsa_mla_decode_mxfp8_args (include/dsa_mla.h): the reference's opus_mla_decode_mxfp8_kargs fields."""
+
+    _fields_ = [
+        ("q_nope", _vp), ("q_scale", _vp), ("q_rope", _vp),
+        ("kv_nope", _vp), ("kv_scale", _vp), ("kv_rope", _vp),
+        ("out", _vp), ("lse", _vp),
+        ("kv_indptr", _vp), ("kv_indices", _vp),
+        ("B", _i32), ("s_q", _i32), ("H", _i32), ("total_tokens", _i32),
+        ("stride_q_nope_b", _i32), ("stride_q_nope_h", _i32),
+        ("stride_q_scale_b", _i32), ("stride_q_scale_h", _i32),
+        ("stride_q_rope_b", _i32), ("stride_q_rope_h", _i32),
+        ("stride_o_b", _i32), ("stride_o_h", _i32),
+        ("stride_kv_nope_page", _i32), ("stride_kv_scale_page", _i32), ("stride_kv_rope_page", _i32),
+        ("max_kv_len", _i32), ("num_splits", _i32),
         ("softmax_scale", ctypes.c_float),
     ]
 
@@ -139,6 +161,8 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.dsa_mla_decode.argtypes = [ctypes.POINTER(DecodeArgs), _vp, ctypes.c_size_t, _vp]
     lib.dsa_mla_decode_csr_workspace_size.argtypes = [ctypes.POINTER(CsrArgs), sz]
     lib.dsa_mla_decode_csr.argtypes = [ctypes.POINTER(CsrArgs), _vp, ctypes.c_size_t, _vp]
+    lib.dsa_mla_decode_mxfp8_workspace_size.argtypes = [ctypes.POINTER(MxArgs), sz]
+    lib.dsa_mla_decode_mxfp8.argtypes = [ctypes.POINTER(MxArgs), _vp, ctypes.c_size_t, _vp]
     lib.dsa_mla_combine.argtypes = [_vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _vp]
     lib.dsa_mla_prefill_workspace_size.argtypes = [ctypes.POINTER(PrefillArgs), sz]
     lib.dsa_mla_prefill.argtypes = [ctypes.POINTER(PrefillArgs), _vp, ctypes.c_size_t, _vp]

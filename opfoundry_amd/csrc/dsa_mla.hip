@@ -67,6 +67,14 @@ constexpr int BF16_LPW = TILE / NWAVE + 1;           // 8 NoPE rows + one 8-row 
 constexpr int FP8_SCALE_OFF = D_NOPE;                // 4 fp32 scales
 constexpr int32_t POOL2 = 1 << 30;                   // row-list tag: a row of the second pool (V4 extend)
 constexpr int FP8_ROPE_OFF = D_NOPE + 16;            // 64 bf16 RoPE values
+// MXFP8 raw slot, one region per stream (every DMA load reads one stream):
+// NoPE codes of row r at 512 r (loads 0..15, two rows each), RoPE at
+// MX_ROPE_OFF + 128 r (loads 16..19, eight rows each), the 16 E8M0 scales at
+// MX_SC_OFF + 16 r (load 20; its upper 32 lanes repeat rows 0..31 into the
+// slot's padding).  Same 21 loads per tile as the 656-B rows.
+constexpr int MX_ROPE_OFF = TILE * D_NOPE;            // 16384
+constexpr int MX_SC_OFF = MX_ROPE_OFF + TILE * 128;   // 20480
+static_assert(MX_SC_OFF + 1024 <= 21 * 1024, "MXFP8 raw slot fits the 656-B slot");
 
 __device__ __forceinline__ int nope_sw(int r) { return (r >> 2) & 3; }
 __device__ __forceinline__ int rope_sw(int r) { return (r >> 1) & 7; }
@@ -75,14 +83,20 @@ __device__ __forceinline__ int rope_sw(int r) { return (r >> 1) & 7; }
 // (bf16: the third tile buffer; fp8: three raw slots), then the row list.
 template <int FMT>
 struct Lay {
-    static constexpr bool FP8 = FMT == DSA_KV_FP8_656;
+    // 656-B rows: fp16 MFMA operands (the per-128 fp32 scale's mantissa is
+    // applied in fp16, so the dequantised values are fp16, not bf16)
+    static constexpr bool F16 = FMT == DSA_KV_FP8_656;
+    // MXFP8 split streams: power-of-two scales, dequantised exactly to bf16
+    static constexpr bool MX = FMT == DSA_KV_MXFP8;
+    // fp8 caches (either): raw-tile ring, dequant stage into the tile buffers
+    static constexpr bool FP8 = F16 || MX;
     static constexpr bool D512 = FMT == DSA_KV_BF16_D512;  // 512-value rows: K = V = the whole row
     static constexpr int RING_BYTES = FP8 ? 3 * RAW_STRIDE : TILE_BYTES;
     static constexpr int LPW = FP8 ? FP8_LPW : (D512 ? TILE / NWAVE : BF16_LPW);  // max DMA loads per wave per tile
     static constexpr int KS = D512 ? KS_NOPE : KS_ALL;    // 16-deep k-steps of QK^T
     // p = exp2(s - m_ref) may grow to 2^TAU over the reference before a
-    // restart: fp16 P (fp8 cache) is finite below 2^16, bf16 P below 2^128.
-    static constexpr float TAU = FP8 ? 15.0f : 100.0f;
+    // restart: fp16 P (656-B cache) is finite below 2^16, bf16 P below 2^128.
+    static constexpr float TAU = F16 ? 15.0f : 100.0f;
 };
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -190,6 +204,15 @@ struct FwdParams {
     int64_t kv2_rows;
     int64_t row_bytes;           // bytes between cache rows (512-value rows)
     const float* attn_sink;      // per-head sink in the softmax denominator, or NULL
+    // MXFP8 split streams: q carries the bf16 RoPE part of Q, kv the fp8 NoPE
+    // codes; strides of the fp8 / E8M0 streams in bytes
+    const unsigned char* q8;     // fp8 NoPE part of Q
+    int64_t q8_sb, q8_st, q8_sh;
+    const unsigned char* qsc;    // E8M0 scales of Q (16 per head)
+    int64_t qsc_sb, qsc_st, qsc_sh;
+    const unsigned char* kv_sc;  // E8M0 scales of the cache rows
+    const unsigned char* kv_ro;  // bf16 RoPE of the cache rows
+    uint32_t kvn_st, kvs_st, kvr_st;   // row strides of kv / kv_sc / kv_ro (bytes)
     __bf16* out;
     int64_t o_sb, o_st, o_sh;
     float* lse;
@@ -255,6 +278,19 @@ __device__ __forceinline__ unsigned bf16x2_to_f16x2(unsigned w) {
     return __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(lo, hi));
 }
 
+// 8 fp8 e4m3 codes (two dwords, low byte first) times 2^(e - 127) -> 8 bf16.
+// Exact: the scale is a power of two and bf16 has fp32's exponent range, so
+// every product is a bf16 value.  The scale operand is the fp32 2^(e - 127)
+// (its exponent field is e); v_cvt_scalef32_pk_bf16_fp8 applies it.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x4 mx_to_bf16(unsigned c0, unsigned c1, unsigned e) {
+    const float sf = __uint_as_float(e << 23);
+    return u32x4{__builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)c0, sf, false)),
+                 __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)c0, sf, true)),
+                 __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)c1, sf, false)),
+                 __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)c1, sf, true))};
+}
+
 // ---------------------------------------------------------------------------
 // Fused sparse-MLA forward: one workgroup per (query token, split).
 // grid = (B, s_q, num_splits), block = 256.
@@ -293,7 +329,23 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // ---- 0. Q fragments (B operand of S^T = K Q^T): lane -> head r32, k-chunk hi ----
     // Issued first so their latency overlaps the index resolution below.
     u32x4 qf[L::KS];
-    {
+    u32x4 q_scales = {0, 0, 0, 0};   // MXFP8: the 16 E8M0 scales of this head's Q
+    if constexpr (L::MX) {
+        // fp8 codes of dims 16ks + 8hi .. +7 in the low half of qf[ks],
+        // converted to bf16 once they have landed; RoPE as bf16
+        const unsigned char* q8p = p.q8 + (int64_t)b * p.q8_sb + (int64_t)t * p.q8_st + (int64_t)head * p.q8_sh + 8 * hi;
+#pragma unroll
+        for (int ks = 0; ks < KS_NOPE; ++ks) {
+            const u32x2 c = *reinterpret_cast<const u32x2*>(q8p + 16 * ks);
+            qf[ks] = u32x4{c[0], c[1], 0u, 0u};
+        }
+        q_scales = *reinterpret_cast<const u32x4*>(p.qsc + (int64_t)b * p.qsc_sb + (int64_t)t * p.qsc_st +
+                                                   (int64_t)head * p.qsc_sh);
+        const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head * p.q_sh + 8 * hi;
+#pragma unroll
+        for (int ks = KS_NOPE; ks < L::KS; ++ks)
+            qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * (ks - KS_NOPE));
+    } else {
         const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head * p.q_sh + 8 * hi;
 #pragma unroll
         for (int ks = 0; ks < L::KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * ks);
@@ -414,9 +466,14 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         } else {
 #pragma unroll
             for (int i = 0; i < FP8_LPW; ++i) {
-                const unsigned c16 = 64 * (wave + NWAVE * i) + ln;   // linear chunk of the raw tile
-                const unsigned rt = __umul24(c16, 1599u) >> 16;     // c16 / 41
-                g.r[i] = rows[rt < TILE - 1 ? rt : TILE - 1];
+                if constexpr (L::MX) {
+                    const int k = wave + NWAVE * i;                      // load of the tile (uniform)
+                    g.r[i] = rows[k < 16 ? 2 * k + (ln >> 5) : (k < 20 ? 8 * (k - 16) + (ln >> 3) : (ln & 31))];
+                } else {
+                    const unsigned c16 = 64 * (wave + NWAVE * i) + ln;   // linear chunk of the raw tile
+                    const unsigned rt = __umul24(c16, 1599u) >> 16;     // c16 / 41
+                    g.r[i] = rows[rt < TILE - 1 ? rt : TILE - 1];
+                }
             }
             g.rope = 0;
         }
@@ -451,10 +508,19 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                 // row 31 (rt clamped to 31 when the row id was fetched, c
                 // < 32) into the slot's padding, so no lane is masked off.
                 const int k = wave + NWAVE * i;
-                const unsigned c16 = 64 * k + ln;
-                const unsigned c = c16 - 41u * (__umul24(c16, 1599u) >> 16);
-                const uint64_t ch = (uint64_t)(uint32_t)g.r[i] * 41u + c;   // 16-byte chunk of the cache
-                lds_dma16(p.kv + (ch << 4), RING + slot * RAW_STRIDE + 1024 * k);
+                const uint64_t row = (uint32_t)g.r[i];
+                if constexpr (L::MX) {
+                    // one stream per load: base and row stride are wave-uniform
+                    const unsigned char* src =
+                        k < 16 ? p.kv + row * p.kvn_st + 16 * (ln & 31)
+                               : (k < 20 ? p.kv_ro + row * p.kvr_st + 16 * (ln & 7) : p.kv_sc + row * p.kvs_st);
+                    lds_dma16(src, RING + slot * RAW_STRIDE + 1024 * k);
+                } else {
+                    const unsigned c16 = 64 * k + ln;
+                    const unsigned c = c16 - 41u * (__umul24(c16, 1599u) >> 16);
+                    const uint64_t ch = row * 41u + c;   // 16-byte chunk of the cache
+                    lds_dma16(p.kv + (ch << 4), RING + slot * RAW_STRIDE + 1024 * k);
+                }
             }
         }
     };
@@ -476,22 +542,30 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 
     // ---- 3. fp8: dequantise a raw slot into a tile buffer (cooperative) ----
     // Nine pieces per tile.  Pieces 0..7: wave w converts row w + 4j; lane l
-    // owns NoPE codes 8l..8l+7 (scale group l/16); fp16 = fp16(code * 2^e) *
-    // fp16(mantissa) where scale = mantissa * 2^e.  Piece 8: RoPE, copied as
-    // bf16 (one 16-byte chunk per thread).
+    // owns NoPE codes 8l..8l+7.  656-B rows (scale group l/16): fp16 =
+    // fp16(code * 2^e) * fp16(mantissa) where scale = mantissa * 2^e.  MXFP8
+    // rows (E8M0 block l/4): bf16 = code * 2^(e - 127), exact.  Piece 8:
+    // RoPE, copied as bf16 (one 16-byte chunk per thread).
     auto deq_load = [&](lds_cptr rb, int j) -> DeqPiece {
         const int ln = opaque(lane);
         DeqPiece d;
         if (j < TILE / NWAVE) {
-            const lds_cptr rr = rb + (wave + NWAVE * j) * FP8_ROW;
+            const int r = wave + NWAVE * j;
+            const lds_cptr rr = rb + r * (L::MX ? D_NOPE : FP8_ROW);
             const u32x2 codes = lds_ld<u32x2>(rr + 8 * ln);
             d.v[0] = codes[0];
             d.v[1] = codes[1];
-            d.v[2] = __float_as_uint(lds_ld<float>(rr + FP8_SCALE_OFF + 4 * (ln >> 4)));
+            if constexpr (L::MX)
+                d.v[2] = lds_ld<unsigned char>(rb + MX_SC_OFF + 16 * r + (ln >> 2));
+            else
+                d.v[2] = __float_as_uint(lds_ld<float>(rr + FP8_SCALE_OFF + 4 * (ln >> 4)));
             d.v[3] = 0;
         } else {
             const int t8 = opaque(tid);
-            d.v = lds_ld<u32x4>(rb + (t8 >> 3) * FP8_ROW + FP8_ROPE_OFF + 16 * (t8 & 7));
+            if constexpr (L::MX)
+                d.v = lds_ld<u32x4>(rb + MX_ROPE_OFF + (t8 >> 3) * 128 + 16 * (t8 & 7));
+            else
+                d.v = lds_ld<u32x4>(rb + (t8 >> 3) * FP8_ROW + FP8_ROPE_OFF + 16 * (t8 & 7));
         }
         return d;
     };
@@ -499,6 +573,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         const int ln = opaque(lane);
         if (j < TILE / NWAVE) {
             const int r = wave + NWAVE * j;
+            if constexpr (L::MX) {
+                lds_st<u32x4>(tb + r * NOPE_STRIDE + 16 * (ln ^ nope_sw(r)), mx_to_bf16(d.v[0], d.v[1], d.v[2]));
+                return;
+            }
             const float sc = __uint_as_float(d.v[2]);
             const _Float16 m16 = (_Float16)__uint_as_float((d.v[2] & 0x007FFFFFu) | 0x3F800000u);
             const f16x2 mm = {m16, m16};
@@ -543,21 +621,28 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         if (s < ntiles) issue_rows(load_rows(s), s);
     if (NPRE < ntiles) gnext = load_rows(NPRE);
 
-    if constexpr (FP8) {
+    if constexpr (L::F16) {
         // the NoPE part of Q is converted to fp16 for the fp16 MFMAs
 #pragma unroll
         for (int ks = 0; ks < KS_NOPE; ++ks)
 #pragma unroll
             for (int w = 0; w < 4; ++w) qf[ks][w] = bf16x2_to_f16x2(qf[ks][w]);
+    } else if constexpr (L::MX) {
+        // fp8 NoPE of Q -> bf16: dims 16ks + 8hi .. +7 lie in scale block ks / 2
+#pragma unroll
+        for (int ks = 0; ks < KS_NOPE; ++ks) {
+            const unsigned e = (q_scales[ks >> 3] >> (8 * ((ks >> 1) & 3))) & 0xFFu;
+            qf[ks] = mx_to_bf16(qf[ks][0], qf[ks][1], e);
+        }
     }
     // Q (and the first gathers) complete before the tile loop: inside the loop
     // the only vector-memory loads are the LDS-DMA gathers counted explicitly.
     wait_vm<0>();
 
-    // P values -> MFMA operand (bf16 for the bf16 cache, fp16 for fp8)
+    // P values -> MFMA operand (fp16 for the 656-B cache, else bf16)
     auto to_p = [&](const float* e) -> u32x4 {
         u32x4 pb;
-        if constexpr (FP8) {
+        if constexpr (L::F16) {
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
                 const f16x2 h = {(_Float16)e[2 * w], (_Float16)e[2 * w + 1]};
@@ -611,7 +696,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         for (int ks = 0; ks < L::KS; ++ks) {
             __builtin_amdgcn_sched_barrier(0);
             f32x16& acc = sacc2[ks & 1];
-            if (FP8 && ks < KS_NOPE) acc = mfma_f16(kb[ks % KPF], qf[ks], acc);
+            if (L::F16 && ks < KS_NOPE) acc = mfma_f16(kb[ks % KPF], qf[ks], acc);
             else acc = mfma_bf16(kb[ks % KPF], qf[ks], acc);
             if (ks + KPF < L::KS) kb[ks % KPF] = lds_ld<u32x4>(k_addr(ks + KPF));
         }
@@ -703,7 +788,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                     __builtin_amdgcn_sched_barrier(0);
                     const u32x4 va_nxt = m + 1 < 4 ? v_frag(u, m + 1) : va_cur;
 #pragma unroll
-                    for (int h = 0; h < NWAVE; ++h) mfma_o<FP8>(o[4 * m + h], va_cur, pbf[h]);
+                    for (int h = 0; h < NWAVE; ++h) mfma_o<L::F16>(o[4 * m + h], va_cur, pbf[h]);
                     if constexpr (FP8) {
                         // piece j: loads in MFMA group j, conversion + store in group j+1
                         const int j = step_i;
@@ -984,7 +1069,8 @@ int validate_decode(const dsa_mla_decode_args* a, int* ns_out, int* chunk_out) {
         if (((uintptr_t)a->q & 15) || ((uintptr_t)a->kv_cache & 15) || ((uintptr_t)a->out & 7))
             return DSA_ERR_BAD_STRIDE;
     }
-    if (a->B > 0 && a->topk == 0 && !a->out) return DSA_ERR_NULL_POINTER;
+    // the kernel reads Q even when no entry is valid: q is needed whenever B > 0
+    if (a->B > 0 && a->topk == 0 && (!a->out || !a->q)) return DSA_ERR_NULL_POINTER;
     *ns_out = ns;
     *chunk_out = chunk;
     return DSA_OK;
@@ -1000,6 +1086,7 @@ int launch_fwd(const FwdParams& fp, int fmt, int B, int s_q, int ns, hipStream_t
     dim3 grid(B, s_q, ns), block(NTHR);
     if (fmt == DSA_KV_BF16) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_BF16>, grid, block, 0, st, fp);
     else if (fmt == DSA_KV_FP8_656) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_FP8_656>, grid, block, 0, st, fp);
+    else if (fmt == DSA_KV_MXFP8) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_MXFP8>, grid, block, 0, st, fp);
     else hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_BF16_D512>, grid, block, 0, st, fp);
     return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_HIP;
 }
@@ -1023,8 +1110,9 @@ int validate_csr(const dsa_mla_decode_csr_args* a, int* ns_out, int* chunk_out) 
     const int chunk = a->max_kv_len == 0 ? 0 : (a->max_kv_len + ns - 1) / ns;
     if (chunk > MAX_CHUNK) return a->num_splits ? DSA_ERR_BAD_SPLITS : DSA_ERR_UNSUPPORTED;
     if (a->B > 0) {
-        if (!a->out || !a->kv_indptr) return DSA_ERR_NULL_POINTER;
-        if (a->max_kv_len > 0 && (!a->q || !a->kv || !a->kv_indices)) return DSA_ERR_NULL_POINTER;
+        // the kernel reads Q even when every list is empty
+        if (!a->out || !a->kv_indptr || !a->q) return DSA_ERR_NULL_POINTER;
+        if (a->max_kv_len > 0 && (!a->kv || !a->kv_indices)) return DSA_ERR_NULL_POINTER;
         if (a->stride_q_b < 0 || a->stride_q_h < 0 || a->stride_o_b < 0 || a->stride_o_h < 0)
             return DSA_ERR_BAD_STRIDE;
         if ((a->stride_q_h % 8) || (a->stride_q_b % 8) || (a->stride_o_h % 4) || (a->stride_o_b % 4))
@@ -1040,11 +1128,44 @@ size_t csr_ws_bytes(const dsa_mla_decode_csr_args* a, int ns) {
     return ns <= 1 || a->B == 0 ? 0 : (size_t)ns * a->B * a->s_q * HEADS * (D_VO + 1) * sizeof(float) + 256;
 }
 
+int validate_mx(const dsa_mla_decode_mxfp8_args* a, int* ns_out, int* chunk_out) {
+    if (!a) return DSA_ERR_NULL_POINTER;
+    if (a->B < 0 || a->s_q <= 0 || a->max_kv_len < 0 || a->total_tokens < 0) return DSA_ERR_BAD_SHAPE;
+    if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
+    if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
+    const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q, a->max_kv_len);
+    const int chunk = a->max_kv_len == 0 ? 0 : (a->max_kv_len + ns - 1) / ns;
+    if (chunk > MAX_CHUNK) return a->num_splits ? DSA_ERR_BAD_SPLITS : DSA_ERR_UNSUPPORTED;
+    if (a->B > 0) {
+        // the kernel reads Q even when every list is empty
+        if (!a->out || !a->kv_indptr || !a->q_nope || !a->q_scale || !a->q_rope) return DSA_ERR_NULL_POINTER;
+        if (a->max_kv_len > 0 && (!a->kv_nope || !a->kv_scale || !a->kv_rope || !a->kv_indices))
+            return DSA_ERR_NULL_POINTER;
+        // fp8 / E8M0 streams: bytes, multiples of 16; bf16 streams: multiples of 8 elements
+        const int32_t b16[] = {a->stride_q_nope_b, a->stride_q_nope_h, a->stride_q_scale_b, a->stride_q_scale_h,
+                               a->stride_kv_nope_page, a->stride_kv_scale_page};
+        const int32_t e8[] = {a->stride_q_rope_b, a->stride_q_rope_h, a->stride_kv_rope_page};
+        for (int32_t v : b16) if (v < 0 || (v % 16)) return DSA_ERR_BAD_STRIDE;
+        for (int32_t v : e8) if (v < 0 || (v % 8)) return DSA_ERR_BAD_STRIDE;
+        if (a->stride_o_b < 0 || a->stride_o_h < 0 || (a->stride_o_b % 4) || (a->stride_o_h % 4))
+            return DSA_ERR_BAD_STRIDE;
+        const void* ptrs[] = {a->q_nope, a->q_scale, a->q_rope, a->kv_nope, a->kv_scale, a->kv_rope};
+        for (const void* q : ptrs) if ((uintptr_t)q & 15) return DSA_ERR_BAD_STRIDE;
+        if ((uintptr_t)a->out & 7) return DSA_ERR_BAD_STRIDE;
+    }
+    *ns_out = ns;
+    *chunk_out = chunk;
+    return DSA_OK;
+}
+size_t mx_ws_bytes(const dsa_mla_decode_mxfp8_args* a, int ns) {
+    return ns <= 1 || a->B == 0 ? 0 : (size_t)ns * a->B * a->s_q * HEADS * (D_VO + 1) * sizeof(float) + 256;
+}
+
 }  // namespace
 
 extern "C" {
 
-int dsa_mla_abi_version(void) { return 3; }
+int dsa_mla_abi_version(void) { return 4; }
 
 const char* dsa_mla_strerror(int code) {
     switch (code) {
@@ -1155,6 +1276,56 @@ int dsa_mla_decode_csr(const dsa_mla_decode_csr_args* a, void* ws, size_t ws_byt
         fp.part_lse = (float*)((char*)ws + (size_t)ns * rows * D_VO * sizeof(float));
     }
     int r = launch_fwd(fp, a->kv_format, a->B, a->s_q, ns, st);
+    if (r || ns == 1) return r;
+    return launch_combine(fp.part_o, fp.part_lse, ns, a->B * a->s_q, HEADS, a->s_q, a->out, fp.o_sb, fp.o_st,
+                          fp.o_sh, a->lse, st);
+}
+int dsa_mla_decode_mxfp8_workspace_size(const dsa_mla_decode_mxfp8_args* a, size_t* bytes) {
+    if (!bytes) return DSA_ERR_NULL_POINTER;
+    int ns, chunk;
+    const int rc = validate_mx(a, &ns, &chunk);
+    if (rc) return rc;
+    *bytes = mx_ws_bytes(a, ns);
+    return DSA_OK;
+}
+int dsa_mla_decode_mxfp8(const dsa_mla_decode_mxfp8_args* a, void* ws, size_t ws_bytes, void* stream) {
+    int ns, chunk;
+    const int rc = validate_mx(a, &ns, &chunk);
+    if (rc) return rc;
+    const size_t need = mx_ws_bytes(a, ns);
+    if (need && (!ws || ws_bytes < need || ((uintptr_t)ws & 15))) return DSA_ERR_WORKSPACE;
+    if (a->B == 0) return DSA_OK;
+    hipStream_t st = (hipStream_t)stream;
+    FwdParams fp{};
+    const int64_t sq = a->s_q;
+    fp.q = (const __bf16*)a->q_rope;
+    fp.q_sb = sq * a->stride_q_rope_b; fp.q_st = a->stride_q_rope_b; fp.q_sh = a->stride_q_rope_h;
+    fp.q8 = (const unsigned char*)a->q_nope;
+    fp.q8_sb = sq * a->stride_q_nope_b; fp.q8_st = a->stride_q_nope_b; fp.q8_sh = a->stride_q_nope_h;
+    fp.qsc = (const unsigned char*)a->q_scale;
+    fp.qsc_sb = sq * a->stride_q_scale_b; fp.qsc_st = a->stride_q_scale_b; fp.qsc_sh = a->stride_q_scale_h;
+    fp.kv = (const unsigned char*)a->kv_nope;
+    fp.kv_sc = (const unsigned char*)a->kv_scale;
+    fp.kv_ro = (const unsigned char*)a->kv_rope;
+    fp.kvn_st = (uint32_t)a->stride_kv_nope_page;
+    fp.kvs_st = (uint32_t)a->stride_kv_scale_page;
+    fp.kvr_st = (uint32_t)a->stride_kv_rope_page * 2u;
+    fp.kv_total_rows = a->total_tokens;
+    fp.block_size = 1;
+    fp.seq_len_default = a->total_tokens;
+    fp.kv_indptr = a->kv_indptr;
+    fp.kv_indices = a->kv_indices;
+    fp.out = (__bf16*)a->out;
+    fp.o_sb = sq * a->stride_o_b; fp.o_st = a->stride_o_b; fp.o_sh = a->stride_o_h;
+    fp.lse = a->lse;
+    fp.B = a->B; fp.s_q = a->s_q; fp.topk = a->max_kv_len; fp.chunk = chunk;
+    fp.scale_log2 = a->softmax_scale * LOG2E;
+    if (ns > 1) {
+        const size_t rows = (size_t)a->B * a->s_q * HEADS;
+        fp.part_o = (float*)ws;
+        fp.part_lse = (float*)((char*)ws + (size_t)ns * rows * D_VO * sizeof(float));
+    }
+    int r = launch_fwd(fp, DSA_KV_MXFP8, a->B, a->s_q, ns, st);
     if (r || ns == 1) return r;
     return launch_combine(fp.part_o, fp.part_lse, ns, a->B * a->s_q, HEADS, a->s_q, a->out, fp.o_sb, fp.o_st,
                           fp.o_sh, a->lse, st);

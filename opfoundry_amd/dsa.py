@@ -189,6 +189,76 @@ def mla_decode_csr(q: torch.Tensor, kv: torch.Tensor, kv_indptr: torch.Tensor,
     return out, lse
 
 
+def make_decode_mxfp8_args(q_nope, q_scale, q_rope, kv_nope, kv_scale, kv_rope, kv_indptr,
+                           kv_indices, sm_scale, out, lse, *, s_q=1, max_kv_len=None, num_splits=0):
+    """dsa_mla_decode_mxfp8_args for split-stream tensors: q_nope uint8 [T, H, 512], q_scale
+    uint8 [T, H, 16], q_rope bf16 [T, H, 64] (T = B * s_q); kv_nope uint8 [rows, 512], kv_scale
+    uint8 [rows, 16], kv_rope bf16 [rows, 64]; every last dim dense."""
+    T, H, _ = q_nope.shape
+    for t, n, w in ((q_nope, "q_nope", 512), (q_scale, "q_scale", 16), (q_rope, "q_rope", 64)):
+        if t.dim() != 3 or t.shape[0] != T or t.shape[1] != H or t.shape[2] != w or t.stride(2) != 1:
+            raise ValueError(f"{n} must be [T, H, {w}] with a dense last dim")
+    rows = kv_nope.shape[0]
+    for t, n, w in ((kv_nope, "kv_nope", 512), (kv_scale, "kv_scale", 16), (kv_rope, "kv_rope", 64)):
+        if t.dim() != 2 or t.shape[0] != rows or t.shape[1] != w or t.stride(1) != 1:
+            raise ValueError(f"{n} must be [rows, {w}] with a dense last dim")
+    B = kv_indptr.numel() - 1
+    if B < 0 or T != B * s_q:
+        raise ValueError("q streams must hold B * s_q query rows (B = kv_indptr.numel() - 1)")
+    if max_kv_len is None:
+        max_kv_len = int((kv_indptr[1:] - kv_indptr[:-1]).max().item()) if B > 0 else 0
+    a = abi.MxArgs()
+    a.q_nope, a.q_scale, a.q_rope = _ptr(q_nope), _ptr(q_scale), _ptr(q_rope)
+    a.kv_nope, a.kv_scale, a.kv_rope = _ptr(kv_nope), _ptr(kv_scale), _ptr(kv_rope)
+    a.out, a.lse = _ptr(out), _ptr(lse)
+    a.kv_indptr, a.kv_indices = _ptr(kv_indptr), _ptr(kv_indices)
+    a.B, a.s_q, a.H, a.total_tokens = B, s_q, H, rows
+    a.stride_q_nope_b, a.stride_q_nope_h = q_nope.stride(0), q_nope.stride(1)
+    a.stride_q_scale_b, a.stride_q_scale_h = q_scale.stride(0), q_scale.stride(1)
+    a.stride_q_rope_b, a.stride_q_rope_h = q_rope.stride(0), q_rope.stride(1)
+    a.stride_o_b, a.stride_o_h = out.stride(0), out.stride(1)
+    a.stride_kv_nope_page, a.stride_kv_scale_page = kv_nope.stride(0), kv_scale.stride(0)
+    a.stride_kv_rope_page = kv_rope.stride(0)
+    a.max_kv_len = max_kv_len
+    a.num_splits = num_splits
+    a.softmax_scale = float(sm_scale)
+    return a
+
+
+def mla_decode_mxfp8(q_nope: torch.Tensor, q_scale: torch.Tensor, q_rope: torch.Tensor,
+                     kv_nope: torch.Tensor, kv_scale: torch.Tensor, kv_rope: torch.Tensor,
+                     kv_indptr: torch.Tensor, kv_indices: torch.Tensor, sm_scale: float,
+                     out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None, *,
+                     s_q: int = 1, max_kv_len: Optional[int] = None, num_splits: int = 0,
+                     workspace: Optional[torch.Tensor] = None,
+                     stream=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Sparse MLA decode on MXFP8 split streams (the reference's -dtype fp8 format), CSR
+    form; returns (out bf16 [B*s_q, H, 512], lse fp32 [B*s_q, H])."""
+    for t, n in ((q_nope, "q_nope"), (q_scale, "q_scale"), (kv_nope, "kv_nope"), (kv_scale, "kv_scale")):
+        _need(t, torch.uint8, n)
+    _need(q_rope, torch.bfloat16, "q_rope")
+    _need(kv_rope, torch.bfloat16, "kv_rope")
+    _need(kv_indptr, torch.int32, "kv_indptr")
+    _need(kv_indices, torch.int32, "kv_indices")
+    T, H, _ = q_nope.shape
+    if out is None:
+        out = torch.empty((T, H, abi.D_VO), dtype=torch.bfloat16, device=q_nope.device)
+    if lse is None:
+        lse = torch.empty((T, H), dtype=torch.float32, device=q_nope.device)
+    a = make_decode_mxfp8_args(q_nope, q_scale, q_rope, kv_nope, kv_scale, kv_rope, kv_indptr,
+                               kv_indices, sm_scale, out, lse, s_q=s_q, max_kv_len=max_kv_len,
+                               num_splits=num_splits)
+    lib = load_library()
+    n = ctypes.c_size_t(0)
+    check(lib.dsa_mla_decode_mxfp8_workspace_size(ctypes.byref(a), ctypes.byref(n)),
+          "dsa_mla_decode_mxfp8_workspace_size")
+    if n.value and (workspace is None or workspace.numel() * workspace.element_size() < n.value):
+        workspace = torch.empty(n.value, dtype=torch.uint8, device=q_nope.device)
+    check(lib.dsa_mla_decode_mxfp8(ctypes.byref(a), _ptr(workspace) if n.value else None, n.value,
+                                   _stream(stream)), "dsa_mla_decode_mxfp8")
+    return out, lse
+
+
 def mla_combine(partial_o: torch.Tensor, partial_lse: torch.Tensor,
                 out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
                 stream=None) -> Tuple[torch.Tensor, torch.Tensor]:

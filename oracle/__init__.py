@@ -20,7 +20,8 @@ import subprocess
 
 import numpy as np
 
-from opfoundry_amd.abi import D_QK, D_V4, D_VO, DecodeArgs, KV_BF16, KV_FP8_656, PrefillArgs, PrefillV4Args
+from opfoundry_amd.abi import (D_QK, D_V4, D_VO, DecodeArgs, KV_BF16, KV_FP8_656, MxArgs, PrefillArgs,
+                               PrefillV4Args)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "_build", "libdsa_oracle.so")
@@ -57,6 +58,9 @@ def lib() -> ctypes.CDLL:
         L.oracle_mla_combine.restype = None
         L.oracle_mla_prefill.argtypes = [ctypes.POINTER(PrefillArgs), ctypes.c_int]
         L.oracle_mla_prefill_v4.argtypes = [ctypes.POINTER(PrefillV4Args), ctypes.c_int]
+        L.oracle_mla_decode_mxfp8.argtypes = [ctypes.POINTER(MxArgs), ctypes.c_int]
+        L.oracle_dequant_row_mxfp8.argtypes = [vp, vp, vp, vp]
+        L.oracle_dequant_row_mxfp8.restype = None
         L.oracle_num_threads.argtypes = [ctypes.c_int]
         _LIB = L
     return _LIB
@@ -223,6 +227,54 @@ def mla_prefill_v4(q, unified_kv, kv, attn_sink, indptr_prefix, indices_prefix, 
     return out, lse
 
 
+def dequant_rows_mxfp8(nope: np.ndarray, scale: np.ndarray, rope: np.ndarray) -> np.ndarray:
+    """MXFP8 split-stream rows (uint8 [n,512], uint8 [n,16], uint16 [n,64]) -> fp32 [n,576]."""
+    nope = np.ascontiguousarray(nope, dtype=np.uint8).reshape(-1, 512)
+    scale = np.ascontiguousarray(scale, dtype=np.uint8).reshape(-1, 16)
+    rope = np.ascontiguousarray(rope, dtype=np.uint16).reshape(-1, 64)
+    out = np.zeros((nope.shape[0], D_QK), np.float32)
+    for r in range(nope.shape[0]):
+        lib().oracle_dequant_row_mxfp8(_p(nope[r]), _p(scale[r]), _p(rope[r]), _p(out[r]))
+    return out
+
+
+def mla_decode_mxfp8(q_nope, q_scale, q_rope, kv_nope, kv_scale, kv_rope, kv_indptr, kv_indices, s_q,
+                     softmax_scale, *, num_threads=0):
+    """Host oracle of dsa_mla_decode_mxfp8 (dense streams): q_* [B*s_q, H, 512 | 16 | 64]
+    (uint8, uint8, uint16), kv_* [rows, 512 | 16 | 64], CSR lists int32.  Returns
+    (O uint16 [B*s_q, H, 512], LSE f32 [B*s_q, H])."""
+    qn = np.ascontiguousarray(q_nope, dtype=np.uint8)
+    qs = np.ascontiguousarray(q_scale, dtype=np.uint8)
+    qr = np.ascontiguousarray(q_rope, dtype=np.uint16)
+    kn = np.ascontiguousarray(kv_nope, dtype=np.uint8).reshape(-1, 512)
+    ks = np.ascontiguousarray(kv_scale, dtype=np.uint8).reshape(-1, 16)
+    kr = np.ascontiguousarray(kv_rope, dtype=np.uint16).reshape(-1, 64)
+    ip = np.ascontiguousarray(kv_indptr, dtype=np.int32)
+    ix = np.ascontiguousarray(kv_indices, dtype=np.int32)
+    if ix.size == 0:
+        ix = np.zeros(1, np.int32)
+    T, H, _ = qn.shape
+    B = ip.size - 1
+    assert T == B * s_q
+    out = np.zeros((T, H, D_VO), np.uint16)
+    lse = np.zeros((T, H), np.float32)
+    a = MxArgs()
+    a.q_nope, a.q_scale, a.q_rope = _p(qn), _p(qs), _p(qr)
+    a.kv_nope, a.kv_scale, a.kv_rope = _p(kn), _p(ks), _p(kr)
+    a.out, a.lse, a.kv_indptr, a.kv_indices = _p(out), _p(lse), _p(ip), _p(ix)
+    a.B, a.s_q, a.H, a.total_tokens = B, s_q, H, kn.shape[0]
+    a.stride_q_nope_b, a.stride_q_nope_h = H * 512, 512
+    a.stride_q_scale_b, a.stride_q_scale_h = H * 16, 16
+    a.stride_q_rope_b, a.stride_q_rope_h = H * 64, 64
+    a.stride_o_b, a.stride_o_h = H * D_VO, D_VO
+    a.stride_kv_nope_page, a.stride_kv_scale_page, a.stride_kv_rope_page = 512, 16, 64
+    a.max_kv_len = int(max((ip[1:] - ip[:-1]).max(initial=0), 1))
+    a.softmax_scale = float(softmax_scale)
+    rc = lib().oracle_mla_decode_mxfp8(ctypes.byref(a), num_threads)
+    assert rc == 0
+    return out, lse
+
+
 def mla_prefill(q, kv, indices, sm_scale, *, causal=False, causal_offset=0, num_threads=0):
     """Host oracle of dsa_mla_prefill: q uint16 [N,H,576], kv uint16 [rows,576] or uint8
     [rows,656], indices int32 [N, topk]."""
@@ -263,6 +315,17 @@ def num_threads(requested: int = 0) -> int:
 def normal_bf16(rng: np.random.Generator, shape) -> np.ndarray:
     """~N(0,1) rounded to bf16 (bit patterns)."""
     return bf16_bits(rng.standard_normal(shape, dtype=np.float32))
+
+
+def mxfp8_rows(rng: np.random.Generator, n: int):
+    """MXFP8 split-stream rows distributed as the reference harness's init_fp8_mla_split
+    (opus_attn/dsa_v32/common/host.cc:207-237): per 32-value block an exponent e in
+    [0, 3], scale byte e + 127, codes e4m3(N(0,1) * 2^-e); RoPE N(0,1) in bf16.
+    Returns (nope uint8 [n,512], scale uint8 [n,16], rope uint16 [n,64])."""
+    e = rng.integers(0, 4, size=(n, 16))
+    x = rng.standard_normal((n, 16, 32), dtype=np.float32) * np.ldexp(1.0, -e)[:, :, None].astype(np.float32)
+    nope = fp8_encode(x.reshape(n, 512))
+    return nope, (e + 127).astype(np.uint8), normal_bf16(rng, (n, 64))
 
 
 def distinct_indices(rng: np.random.Generator, high: int, k: int) -> np.ndarray:

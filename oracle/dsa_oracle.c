@@ -20,6 +20,8 @@
  *                                   the decode core)
  *   - V4 prefill (prefix + extend
  *     pools, attention sink, D=512) opus_attn/dsa_v4/common/mla_v4_host.cc:455-532
+ *   - MXFP8 split-stream decode ... opus_attn/dsa_v32/common/host.cc:418-429 (dequant),
+ *                                   :459-506 (CSR rows, count-based MTP causality)
  *   - split combine ............... opus_attn/dsa_v32/common/mla_reduce.hpp:6-156
  *   - threading ................... opus_attn/dsa_v32/common/parallel.h:11-57
  * generalised to the top-k index form (-1 padding, seq_len and causal bounds,
@@ -479,4 +481,64 @@ int oracle_mla_prefill(const dsa_mla_prefill_args* a, int nthreads) {
     prefill_ctx c = {a};
     const size_t scratch = (size_t)D_QK + a->topk + (size_t)a->topk * D_QK;
     return run_pool(prefill_task, &c, a->N, scratch, nthreads);
+}
+
+/* ------------------------------------------------------- MXFP8 decode */
+
+/*
+ * dequant_mla_row_fp8 (opus_attn/dsa_v32/common/host.cc:418-429): NoPE dim d
+ * = e4m3(code_d) * 2^(scale[d / 32] - 127) (ldexp of the E8M0 byte), RoPE
+ * bf16 widened.  Strides in elements of each stream.
+ */
+void oracle_dequant_row_mxfp8(const uint8_t* nope, const uint8_t* scale, const uint16_t* rope, float* out) {
+    for (int d = 0; d < D_NOPE; ++d)
+        out[d] = oracle_fp8_e4m3_decode(nope[d]) * ldexpf(1.0f, (int)scale[d / 32] - 127);
+    for (int j = 0; j < D_ROPE; ++j) out[D_NOPE + j] = oracle_bf16_to_f32(rope[j]);
+}
+
+typedef struct {
+    const dsa_mla_decode_mxfp8_args* a;
+} mx_ctx;
+
+/*
+ * mla_decode_attention_ref_fp8 (host.cc:459-506) for query token row i =
+ * b * s_q + t: rows kv_indices[kv_indptr[b] + p] for p < kv_indptr[b+1] -
+ * kv_indptr[b] - (s_q - 1 - t) (:481-482), every row and Q dequantised to
+ * fp32 (:493-502), then the decode attention core (:431-457) with
+ * softmax_scale as a parameter.  A row outside [0, total_tokens) is skipped
+ * (the reference reads it unchecked).
+ */
+static void mx_task(void* vctx, int64_t i, float* scratch) {
+    const dsa_mla_decode_mxfp8_args* a = ((const mx_ctx*)vctx)->a;
+    const int b = (int)(i / a->s_q), t = (int)(i % a->s_q);
+    float* q = scratch;
+    float* scores = q + D_QK;
+    float* kv = scores + a->max_kv_len;
+    const int32_t kb = a->kv_indptr[b];
+    const int32_t count = a->kv_indptr[b + 1] - kb - (a->s_q - 1 - t);
+    int n = 0;
+    for (int32_t p = 0; p < count && p < a->max_kv_len; ++p) {
+        const int32_t r = a->kv_indices[kb + p];
+        if (r < 0 || r >= a->total_tokens) continue;
+        oracle_dequant_row_mxfp8((const uint8_t*)a->kv_nope + (int64_t)r * a->stride_kv_nope_page,
+                                 (const uint8_t*)a->kv_scale + (int64_t)r * a->stride_kv_scale_page,
+                                 (const uint16_t*)a->kv_rope + (int64_t)r * a->stride_kv_rope_page,
+                                 kv + (size_t)n * D_QK);
+        ++n;
+    }
+    for (int h = 0; h < a->H; ++h) {
+        oracle_dequant_row_mxfp8((const uint8_t*)a->q_nope + i * a->stride_q_nope_b + h * a->stride_q_nope_h,
+                                 (const uint8_t*)a->q_scale + i * a->stride_q_scale_b + h * a->stride_q_scale_h,
+                                 (const uint16_t*)a->q_rope + i * a->stride_q_rope_b + h * a->stride_q_rope_h,
+                                 q);
+        uint16_t* o = (uint16_t*)a->out + i * a->stride_o_b + h * a->stride_o_h;
+        attention_core(q, kv, n, a->softmax_scale, scores, o, NULL, a->lse ? a->lse + i * a->H + h : NULL);
+    }
+}
+
+/* Final MXFP8 decode: bf16 O and fp32 LSE (host pointers); max_kv_len bounds every list. */
+int oracle_mla_decode_mxfp8(const dsa_mla_decode_mxfp8_args* a, int nthreads) {
+    mx_ctx c = {a};
+    const size_t scratch = (size_t)D_QK + a->max_kv_len + (size_t)a->max_kv_len * D_QK;
+    return run_pool(mx_task, &c, (int64_t)a->B * a->s_q, scratch, nthreads);
 }
