@@ -7,8 +7,10 @@ are already resident in HBM.  Default workload: BASELINE config 3 (the one the
 north-star target is quoted on) - fp8 656-byte KV rows, batch 128, MTP s_q = 2,
 128 heads, top-k 2048, seq_len 65536 paged at 64 rows, causal.  The JSON line
 also carries config 5 (bf16 sparse prefill, 8192 x 128 heads x top-k 2048) in
-TFLOP/s, the dominant kernel's roofline, and the CPU oracle timed on a bounded
-sample of the same workload on this host.
+TFLOP/s, the same decode on MXFP8 split streams (the reference's own -dtype fp8
+format, C3-shaped: B=128, s_q=2, 2048 rows per token), the dominant kernel's
+roofline for each, and the CPU oracle timed on a bounded sample of each
+workload on this host.
 
 Algorithmic work (V = valid (query, index) pairs):
   FLOPs = 2 * 128 * (576 + 512) * V
@@ -42,6 +44,9 @@ CONFIGS = {
     "c4": dict(kind="decode", B=4, s_q=1, seq=None, block=64, topk=2048, pad=0, fp8=False,
                causal=False, splits=8),
     "c5": dict(kind="prefill", N=8192, topk=2048),
+    # MXFP8 split streams (the reference's -dtype fp8 format), C3-shaped: the two tokens of an
+    # MTP pair see 2047 and 2048 rows of their batch's CSR list (count-based causality)
+    "mx": dict(kind="mxfp8", B=128, s_q=2, rows=2048),
 }
 NAMES = {
     "c1": "bf16 sparse MLA decode B=2 H=128 top-k 2048 (256 pad) flat KV 8192",
@@ -49,6 +54,8 @@ NAMES = {
     "c3": "fp8-KV(656B) sparse MLA decode B=128 s_q=2 (MTP) H=128 top-k 2048 paged(64) seq 65536 causal",
     "c4": "bf16 split-top-k decode B=4 H=128 top-k<=2048 seq U[1024,131072] 8 splits + combine",
     "c5": "bf16 sparse MLA prefill N=8192 H=128 top-k 2048 from [0,t]",
+    "mx": ("MXFP8 split-stream sparse MLA decode (E8M0 per 32, CSR) B=128 s_q=2 (MTP) H=128, "
+           "2048-row lists from a shuffled page table"),
 }
 
 
@@ -142,6 +149,90 @@ def prefill_step(p, dev):
     nbytes = dsa.prefill_workspace_size(a)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes else None
     return prepared_prefill(a, ws), (pout, plse, a, ws)
+
+
+def make_mx(cfg, dev, seed=2041):
+    """MXFP8 split streams drawn as init_fp8_mla_split (opus_attn/dsa_v32/common/host.cc:207-237):
+    per 32-value block e in [0, 3], scale byte e + 127, codes e4m3(N(0,1) * 2^-e); RoPE N(0,1)
+    bf16.  The page table is a shuffled permutation of all rows (host.cc:239-262)."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    B, s_q, L = cfg["B"], cfg["s_q"], cfg["rows"]
+
+    def streams(n):
+        e = torch.randint(0, 4, (n, 16), generator=g, device=dev)
+        x = torch.randn((n, 16, 32), generator=g, device=dev) * torch.exp2(-e.float())[:, :, None]
+        nope = x.reshape(n, 512).to(torch.float8_e4m3fn).view(torch.uint8)
+        rope = torch.randn((n, 64), generator=g, device=dev).to(torch.bfloat16)
+        return nope, (e + 127).to(torch.uint8), rope
+
+    total = B * L
+    kv = streams(total)
+    qn, qs, qr = streams(B * s_q * H)
+    q = (qn.view(B * s_q, H, 512), qs.view(B * s_q, H, 16), qr.view(B * s_q, H, 64))
+    indptr = (torch.arange(B + 1, device=dev, dtype=torch.int32) * L)
+    indices = torch.randperm(total, generator=g, device=dev).to(torch.int32)
+    torch.cuda.synchronize()
+    return dict(q=q, kv=kv, indptr=indptr, indices=indices, s_q=s_q, L=L)
+
+
+def prepared_mx(a, ws):
+    import ctypes
+    import torch
+    from opfoundry_amd.abi import check, load_library
+    fn = load_library().dsa_mla_decode_mxfp8
+    ap = ctypes.byref(a)
+    wp, wb = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
+    st = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        rc = fn(ap, wp, wb, st)
+        if rc:
+            check(rc, "dsa_mla_decode_mxfp8")
+    return step
+
+
+def mx_step(m, dev):
+    """(step, buffers, num_splits) for one MXFP8 decode call through the C ABI."""
+    import ctypes
+    import torch
+    from opfoundry_amd import dsa
+    from opfoundry_amd.abi import check, load_library
+    T = m["q"][0].shape[0]
+    out = torch.empty((T, H, D_VO), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((T, H), dtype=torch.float32, device=dev)
+    a = dsa.make_decode_mxfp8_args(*m["q"], *m["kv"], m["indptr"], m["indices"], SM_SCALE, out, lse,
+                                   s_q=m["s_q"], max_kv_len=m["L"])
+    n = ctypes.c_size_t(0)
+    check(load_library().dsa_mla_decode_mxfp8_workspace_size(ctypes.byref(a), ctypes.byref(n)),
+          "dsa_mla_decode_mxfp8_workspace_size")
+    ws = torch.empty(n.value, dtype=torch.uint8, device=dev) if n.value else None
+    return prepared_mx(a, ws), (out, lse, a, ws), (1 if not n.value else None)
+
+
+def cpu_baseline_mx(m, sample_batches):
+    """The C oracle on the first `sample_batches` batches (both MTP tokens, all heads),
+    scaled to the full step."""
+    import numpy as np
+    import torch
+    import oracle
+    s_q, L = m["s_q"], m["L"]
+    B = m["indptr"].numel() - 1
+    nb = min(sample_batches, B)
+    q = tuple(x[:nb * s_q].cpu().numpy() for x in m["q"][:2]) + \
+        (m["q"][2][:nb * s_q].cpu().view(torch.int16).numpy().view(np.uint16),)
+    kv = (m["kv"][0].cpu().numpy(), m["kv"][1].cpu().numpy(),
+          m["kv"][2].cpu().view(torch.int16).numpy().view(np.uint16))
+    ip = m["indptr"][:nb + 1].cpu().numpy()
+    ix = m["indices"][:nb * L].cpu().numpy()
+    nt = oracle.num_threads()
+    t0 = time.perf_counter()
+    oracle.mla_decode_mxfp8(*q, *kv, ip, ix, s_q, SM_SCALE, num_threads=nt)
+    dt = time.perf_counter() - t0
+    return dict(value=dt * B / nb * 1e6, unit="us/step", cores=nt, kind="port",
+                sample=f"{nb} of {B} batches ({nb * s_q} query tokens, all 128 heads), {dt:.2f} s "
+                       f"measured, scaled x{B / nb:.1f} to one step")
 
 
 def count_valid(d) -> int:
@@ -309,6 +400,9 @@ def main():
     ap.add_argument("--config", default="c3", choices=list(CONFIGS),
                     help="decode workload of the JSON line (c5 only with --kernel-only)")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-mx", action="store_true")
+    ap.add_argument("--cpu-mx-sample", type=int, default=64,
+                    help="batches of the mx step (both MTP tokens) the CPU oracle runs")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=256,
                     help="query tokens of the decode step the CPU oracle runs (256 = all of c3)")
@@ -338,6 +432,14 @@ def main():
         ms = time_steps(lambda: dst.copy_(src), args.steps, args.warmup)
         print(json.dumps({"copy_bytes": n, "ms_per_copy": ms,
                           "GBps_read_plus_write": 2 * n / (ms * 1e-3) / 1e9}))
+        return
+    if cfg["kind"] == "mxfp8":
+        if not args.kernel_only:
+            ap.error("--config mx is reported inside the default JSON line; use it with --kernel-only")
+        log("building mx inputs")
+        m = make_mx(cfg, dev)
+        ms = time_steps(mx_step(m, dev)[0], args.steps, args.warmup)
+        print(json.dumps({"config": args.config, "ms_per_step": ms}))
         return
     if cfg["kind"] == "prefill":
         if not args.kernel_only:
@@ -411,6 +513,37 @@ def main():
         res["cpu_baseline"] = cpu_baseline_decode(d, cfg["fp8"], args.cpu_sample, B * s_q)
     del d
     torch.cuda.empty_cache()
+
+    if not args.no_mx:
+        log("building mx (MXFP8 split-stream) inputs")
+        m = make_mx(CONFIGS["mx"], dev)
+        mstep, keep, mns = mx_step(m, dev)
+        mms = time_steps(mstep, args.steps, args.warmup)
+        mk_ms = kernel_avg_ms(mstep, max(10, args.steps // 2)) if mns == 1 else None
+        del keep
+        T = m["q"][0].shape[0]
+        L = m["L"]
+        mV = sum(L - (m["s_q"] - 1 - t) for t in range(m["s_q"])) * (T // m["s_q"])
+        # both tokens of an MTP pair share their batch's list: each row counts once
+        nb = T // m["s_q"]
+        m_bytes = T * H * (512 + 16 + 128) + nb * L * (656 + 4) + T * H * D_VO * 2 + T * H * 4
+        mdom = mk_ms if mk_ms is not None else mms
+        mach = m_bytes / (mdom * 1e-3) / 1e9
+        res["mxfp8"] = {"workload": f"mx: {NAMES['mx']}", "us_per_step": round(mms * 1e3, 3),
+                        "dtype": "MXFP8 (e4m3 + E8M0) KV and Q -> exact bf16 dequant, bf16 MFMA, f32 accumulate",
+                        "valid_pairs": mV, "hbm_TBps": round(m_bytes / (mms * 1e-3) / 1e12, 3),
+                        "roofline": {"bound": "hbm", "achieved": round(mach, 1), "peak": HBM_PEAK_GBS,
+                                     "unit": "GB/s", "frac": round(mach / HBM_PEAK_GBS, 4),
+                                     "traffic": profiled_traffic("dsa_mla_fwd_mxfp8_mx_traffic.txt"),
+                                     "kernel": "dsa_mla_fwd_kernel<mxfp8>",
+                                     "kernel_avg_us": round(mdom * 1e3, 3), "alg_bytes": m_bytes,
+                                     "mfma_frac": round(FLOP_PER_PAIR * mV / (mdom * 1e-3) / 1e12
+                                                        / BF16_PEAK_TFLOPS, 4)}}
+        if not args.no_cpu:
+            log("CPU baseline (oracle) on an MXFP8 sample")
+            res["mxfp8"]["cpu_baseline"] = cpu_baseline_mx(m, args.cpu_mx_sample)
+        del m
+        torch.cuda.empty_cache()
 
     if not args.no_prefill:
         log("building c5 prefill inputs")
