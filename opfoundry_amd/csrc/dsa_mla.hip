@@ -907,9 +907,19 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     for (int h = 0; h < NWAVE; ++h) inv[h] = s_l[32 * h + r32];
     const int d0 = 128 * wave + 4 * hi;   // this lane's first output dim in block (m, g)
     if (p.part_o == nullptr) {
+        // O through LDS, 32 heads at a time (the heads of o[4m + h]), so that
+        // every global store of a wave writes one whole 1 KB head row: written
+        // straight from the accumulators, each store would scatter 16-byte
+        // pieces over 32 rows.  Rows are OUT_STRIDE bytes apart in the stage
+        // (a 16-byte pad staggers the banks); the two tile buffers alternate.
+        constexpr int OUT_STRIDE = D_VO * 2 + 16;
+        static_assert(32 * OUT_STRIDE <= TILE_BYTES, "O stage fits a tile buffer");
+        __bf16* const orow = p.out + (int64_t)b * p.o_sb + (int64_t)t * p.o_st;
+        // 16-byte stores need 16-byte aligned rows; the API allows 8
+        const bool o16 = ((p.o_sb | p.o_st | p.o_sh) & 7) == 0 && ((uintptr_t)p.out & 15) == 0;
 #pragma unroll
         for (int h = 0; h < NWAVE; ++h) {
-            __bf16* op = p.out + (int64_t)b * p.o_sb + (int64_t)t * p.o_st + (int64_t)(32 * h + r32) * p.o_sh + d0;
+            const lds_ptr stg = (h & 1) ? T1 : T0;
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
 #pragma unroll
@@ -918,7 +928,21 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                     const f32x4 v4 = {a[4 * g] * inv[h], a[4 * g + 1] * inv[h], a[4 * g + 2] * inv[h],
                                       a[4 * g + 3] * inv[h]};
                     const bf16x4 bv = __builtin_convertvector(v4, bf16x4);
-                    *reinterpret_cast<u32x2*>(op + 32 * m + 8 * g) = __builtin_bit_cast(u32x2, bv);
+                    lds_st<u32x2>(stg + r32 * OUT_STRIDE + 2 * (d0 + 32 * m + 8 * g), __builtin_bit_cast(u32x2, bv));
+                }
+            }
+            __syncthreads();
+            // wave w writes head rows 8w .. 8w+7 of this block, 16 bytes per lane
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int r = 8 * wave + k;
+                const u32x4 v = lds_ld<u32x4>(stg + r * OUT_STRIDE + 16 * lane);
+                __bf16* const dst = orow + (int64_t)(32 * h + r) * p.o_sh + 8 * lane;
+                if (o16) {
+                    *reinterpret_cast<u32x4*>(dst) = v;
+                } else {
+                    reinterpret_cast<u32x2*>(dst)[0] = u32x2{v[0], v[1]};
+                    reinterpret_cast<u32x2*>(dst)[1] = u32x2{v[2], v[3]};
                 }
             }
         }
