@@ -12,6 +12,11 @@ format, C3-shaped: B=128, s_q=2, 2048 rows per token), the dominant kernel's
 roofline for each, and the CPU oracle timed on a bounded sample of each
 workload on this host.
 
+Warm-up: by default at least 10 steps and 0.15 s of back-to-back calls per
+workload before the timed steps (the GPU takes tens of ms of sustained load to
+settle; the first ~30 ms of a decode run are up to 30 % slower).  The JSON line
+reports the warm-up step count used.
+
 Algorithmic work (V = valid (query, index) pairs):
   FLOPs = 2 * 128 * (576 + 512) * V
   bytes = Q + V * row_bytes + O + LSE + indices   (row_bytes 656 fp8 / 1152 bf16)
@@ -296,11 +301,31 @@ def profiled_traffic(name):
 
 # ------------------------------------------------------------------ timing
 
+WARM_SECONDS = 0.15
+
+
+def warm_up(fn, warmup):
+    """Untimed warm-up: exactly `warmup` steps, or (None) at least 10 steps and WARM_SECONDS of
+    back-to-back calls.  The MI355X takes tens of ms of sustained load to settle: the first
+    ~30 ms of a decode run are up to 30 % slower than its steady state.  Returns the count."""
+    import torch
+    if warmup is not None:
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        return warmup
+    n, t0 = 0, time.perf_counter()
+    while n < 10 or time.perf_counter() - t0 < WARM_SECONDS:
+        for _ in range(10):
+            fn()
+        n += 10
+        torch.cuda.synchronize()
+    return n
+
+
 def time_steps(fn, steps, warmup):
     import torch
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
+    warm_up(fn, warmup)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -396,7 +421,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warm-up steps (default: at least 10 steps and 0.15 s of "
+                         "back-to-back calls, until the GPU's clocks have settled)")
     ap.add_argument("--config", default="c3", choices=list(CONFIGS),
                     help="decode workload of the JSON line (c5 only with --kernel-only)")
     ap.add_argument("--no-prefill", action="store_true")
@@ -464,8 +491,9 @@ def main():
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     step = prepared_decode(a, ws)
 
-    log(f"timing {args.steps} steps after {args.warmup} warm-up (splits={ns})")
-    ms = time_steps(step, args.steps, args.warmup)
+    log(f"timing {args.steps} steps after warm-up (splits={ns})")
+    n_warm = warm_up(step, args.warmup)
+    ms = time_steps(step, args.steps, 0)
     if args.kernel_only:
         print(json.dumps({"config": args.config, "ms_per_step": ms}))
         return
@@ -476,9 +504,11 @@ def main():
     alg_bytes = (B * s_q * H * D_QK * 2 + V * row_bytes + B * s_q * H * D_VO * 2 + B * s_q * H * 4
                  + B * s_q * topk * 4)
     flops = FLOP_PER_PAIR * V
-    # dominant kernel: the fused decode kernel (the only one when unsplit)
-    k_ms = kernel_avg_ms(step, max(10, args.steps // 2)) if ns == 1 else None
-    dom_ms = k_ms if k_ms is not None else ms
+    # dominant kernel: the fused decode kernel.  Unsplit, a step is that one kernel and its
+    # launch duration is the HIP-event average over the timed region (event pairs around
+    # single launches would add a cache flush to each).  Split, the step also holds the
+    # combine kernel: time the fused kernel alone with per-launch events.
+    dom_ms = ms if ns == 1 else kernel_avg_ms(step, max(10, args.steps // 2))
     achieved = alg_bytes / (dom_ms * 1e-3) / 1e9
     res = {
         "metric": "sparse-MLA decode us/step + achieved HBM TB/s; prefill TFLOP/s (1 MI355X)",
@@ -486,7 +516,7 @@ def main():
         "unit": "us/step",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": n_warm,
         "ms_per_step": round(ms, 5),
         "higher_is_better": False,
         "scaling": "weak",
@@ -518,8 +548,8 @@ def main():
         log("building mx (MXFP8 split-stream) inputs")
         m = make_mx(CONFIGS["mx"], dev)
         mstep, keep, mns = mx_step(m, dev)
-        mms = time_steps(mstep, args.steps, args.warmup)
-        mk_ms = kernel_avg_ms(mstep, max(10, args.steps // 2)) if mns == 1 else None
+        mms = time_steps(mstep, args.steps, args.warmup)   # warm-up as the decode leg
+        mk_ms = mms if mns == 1 else None
         del keep
         T = m["q"][0].shape[0]
         L = m["L"]
@@ -550,8 +580,8 @@ def main():
         p = make_prefill(CONFIGS["c5"], dev)
         pstep, keep = prefill_step(p, dev)
         psteps = max(3, args.steps // 5)
-        pms = time_steps(pstep, psteps, 2)
-        pk_ms = kernel_avg_ms(pstep, psteps)
+        pms = time_steps(pstep, psteps, None if args.warmup is None else 2)
+        pk_ms = pms       # one kernel per step: the timed region's average launch
         del keep
         pV = int((p["idx"] >= 0).sum())
         pfl = FLOP_PER_PAIR * pV
