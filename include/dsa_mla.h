@@ -56,12 +56,16 @@ extern "C" {
 #define DSA_MLA_BF16_ROW_BYTES 1152
 #define DSA_MLA_MAX_SPLITS 64
 #define DSA_MLA_D_V4 512       /* V4 prefill head dim: K = V = a 512-value row */
+#define DSA_MLA_V4_NOPE 448    /* V4 fp8 rows: fp8 NoPE values (then 64 bf16 RoPE) */
+#define DSA_MLA_V4_NOPE_BYTES 512  /* V4 fp8 NoPE stream row: 448 codes, 14 E8M0, pad */
 
 typedef enum {
     DSA_KV_BF16 = 0,
     DSA_KV_FP8_656 = 1,
     DSA_KV_BF16_D512 = 2,      /* 512 x bf16 rows (V4 prefill only) */
-    DSA_KV_MXFP8 = 3           /* MXFP8 split streams (dsa_mla_decode_mxfp8 only) */
+    DSA_KV_MXFP8 = 3,          /* MXFP8 split streams (dsa_mla_decode_mxfp8 only) */
+    DSA_KV_MXFP8_V4 = 4        /* V4 fp8 rows: 448 e4m3 + 14 E8M0 + pad | 64 bf16 RoPE
+                                  (dsa_mla_prefill_v4_fp8 only) */
 } dsa_kv_format;
 
 enum {
@@ -317,6 +321,49 @@ typedef struct {
 } dsa_mla_prefill_v4_args;
 
 int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* args, void* stream);
+
+/*
+ * DeepSeek-V4 sparse prefill on fp8 rows: the argument set of
+ * opus_mla_v4_prefill_fp8_kargs (opus_attn/dsa_v4/common/mla_v4_kargs.h:31-58)
+ * plus an optional LSE output and the max_rows bound.  Replaces
+ * mla_v4_prefill_launch with that kargs (mla_v4_host.cc:38-47).
+ * A row (and Q per head) is two streams:
+ *   nope : 512 bytes = 448 e4m3fn codes, 14 E8M0 scales (one per 32 values),
+ *          2 pad bytes and 48 more (the reference fills them with 0xFF)
+ *   rope : 64 bf16 values
+ * Value d < 448 = float(e4m3(code_d)) * 2^(scale[d / 32] - 127); values
+ * 448..511 are the RoPE values (decode_dsa_row_fp8, mla_v4_host.cc:443-453).
+ * K = V = the 512-value row; softmax, sink, pools, CSR lists, skipping and
+ * LSE exactly as in dsa_mla_prefill_v4.  Strides in elements of each stream
+ * (bytes for nope, bf16 elements for rope and out); nope pointers and strides
+ * 16-byte aligned, rope strides multiples of 8, out strides of 4.  The kernel
+ * never reads the pad bytes, nor any row the lists do not name.
+ */
+typedef struct {
+    const void* q_nope;
+    const void* q_rope;
+    const void* unified_kv_nope;
+    const void* unified_kv_rope;
+    const void* kv_nope;
+    const void* kv_rope;
+    const float* attn_sink;
+    void* out;
+    float* lse;
+    const int32_t* kv_indptr_prefix;
+    const int32_t* kv_indices_prefix;
+    const int32_t* kv_indptr_extend;
+    const int32_t* kv_indices_extend;
+    int32_t N, H;
+    int32_t total_pages, total_tokens;
+    int32_t stride_q_nope_n, stride_q_nope_h;
+    int32_t stride_q_rope_n, stride_q_rope_h;
+    int32_t stride_o_n, stride_o_h;
+    int32_t stride_kv_nope_page, stride_kv_rope_page;
+    int32_t max_rows;
+    float softmax_scale;
+} dsa_mla_prefill_v4_fp8_args;
+
+int dsa_mla_prefill_v4_fp8(const dsa_mla_prefill_v4_fp8_args* args, void* stream);
 
 /*
  * fp8 cache writer: quantise n_rows bf16 latent rows (576 values, row stride

@@ -20,6 +20,8 @@ KV_BF16 = 0
 KV_FP8_656 = 1
 KV_BF16_D512 = 2
 KV_MXFP8 = 3
+KV_MXFP8_V4 = 4
+V4_NOPE = 448
 D_V4 = 512
 
 DSA_OK = 0
@@ -47,12 +49,13 @@ EXPORTED_SYMBOLS = (
     "dsa_mla_prefill_workspace_size",
     "dsa_mla_prefill",
     "dsa_mla_prefill_v4",
+    "dsa_mla_prefill_v4_fp8",
     "dsa_kv_quantize_fp8",
     "dsa_mla_strerror",
     "dsa_mla_abi_version",
 )
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -135,6 +138,25 @@ class PrefillV4Args(ctypes.Structure):
     ]
 
 
+class PrefillV4Fp8Args(ctypes.Structure):
+    """dsa_mla_prefill_v4_fp8_args (include/dsa_mla.h): the fields of opus_mla_v4_prefill_fp8_kargs."""
+
+    _fields_ = [
+        ("q_nope", _vp), ("q_rope", _vp),
+        ("unified_kv_nope", _vp), ("unified_kv_rope", _vp),
+        ("kv_nope", _vp), ("kv_rope", _vp),
+        ("attn_sink", _vp), ("out", _vp), ("lse", _vp),
+        ("kv_indptr_prefix", _vp), ("kv_indices_prefix", _vp),
+        ("kv_indptr_extend", _vp), ("kv_indices_extend", _vp),
+        ("N", _i32), ("H", _i32), ("total_pages", _i32), ("total_tokens", _i32),
+        ("stride_q_nope_n", _i32), ("stride_q_nope_h", _i32),
+        ("stride_q_rope_n", _i32), ("stride_q_rope_h", _i32),
+        ("stride_o_n", _i32), ("stride_o_h", _i32),
+        ("stride_kv_nope_page", _i32), ("stride_kv_rope_page", _i32),
+        ("max_rows", _i32), ("softmax_scale", ctypes.c_float),
+    ]
+
+
 class DsaError(RuntimeError):
     def __init__(self, code: int, where: str):
         self.code = code
@@ -167,6 +189,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.dsa_mla_prefill_workspace_size.argtypes = [ctypes.POINTER(PrefillArgs), sz]
     lib.dsa_mla_prefill.argtypes = [ctypes.POINTER(PrefillArgs), _vp, ctypes.c_size_t, _vp]
     lib.dsa_mla_prefill_v4.argtypes = [ctypes.POINTER(PrefillV4Args), _vp]
+    lib.dsa_mla_prefill_v4_fp8.argtypes = [ctypes.POINTER(PrefillV4Fp8Args), _vp]
     lib.dsa_kv_quantize_fp8.argtypes = [_vp, _i64, _i64, _vp, _i64, _vp, _vp]
     lib.dsa_mla_strerror.argtypes = [ctypes.c_int]
     lib.dsa_mla_strerror.restype = ctypes.c_char_p

@@ -86,11 +86,19 @@ struct Lay {
     // 656-B rows: fp16 MFMA operands (the per-128 fp32 scale's mantissa is
     // applied in fp16, so the dequantised values are fp16, not bf16)
     static constexpr bool F16 = FMT == DSA_KV_FP8_656;
-    // MXFP8 split streams: power-of-two scales, dequantised exactly to bf16
-    static constexpr bool MX = FMT == DSA_KV_MXFP8;
-    // fp8 caches (either): raw-tile ring, dequant stage into the tile buffers
+    // MXFP8 split streams (E8M0 scales, dequantised exactly to bf16): the
+    // V3.2 decode format, or the V4 format (448 fp8 NoPE values whose 14
+    // scales follow them in the same 512-byte stream row, then 64 bf16 RoPE)
+    static constexpr bool MX = FMT == DSA_KV_MXFP8 || FMT == DSA_KV_MXFP8_V4;
+    static constexpr bool V4MX = FMT == DSA_KV_MXFP8_V4;
+    // fp8 caches (any): raw-tile ring, dequant stage into the tile buffers
     static constexpr bool FP8 = F16 || MX;
-    static constexpr bool D512 = FMT == DSA_KV_BF16_D512;  // 512-value rows: K = V = the whole row
+    // 512-value rows: K = V = the whole row (V4 prefill)
+    static constexpr bool D512 = FMT == DSA_KV_BF16_D512 || FMT == DSA_KV_MXFP8_V4;
+    // LDS-DMA loads per raw tile: V4 rows need no separate scale load
+    static constexpr int LOADS = V4MX ? 20 : FP8_LOADS;
+    // k-steps of QK^T whose Q values come from the fp8 NoPE stream
+    static constexpr int Q8_KS = V4MX ? DSA_MLA_V4_NOPE / 16 : KS_NOPE;
     static constexpr int RING_BYTES = FP8 ? 3 * RAW_STRIDE : TILE_BYTES;
     static constexpr int LPW = FP8 ? FP8_LPW : (D512 ? TILE / NWAVE : BF16_LPW);  // max DMA loads per wave per tile
     static constexpr int KS = D512 ? KS_NOPE : KS_ALL;    // 16-deep k-steps of QK^T
@@ -212,6 +220,7 @@ struct FwdParams {
     int64_t qsc_sb, qsc_st, qsc_sh;
     const unsigned char* kv_sc;  // E8M0 scales of the cache rows
     const unsigned char* kv_ro;  // bf16 RoPE of the cache rows
+    const unsigned char* kv2_ro; // bf16 RoPE of the second pool's rows (V4 fp8)
     uint32_t kvn_st, kvs_st, kvr_st;   // row strides of kv / kv_sc / kv_ro (bytes)
     __bf16* out;
     int64_t o_sb, o_st, o_sh;
@@ -335,7 +344,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         // converted to bf16 once they have landed; RoPE as bf16
         const unsigned char* q8p = p.q8 + (int64_t)b * p.q8_sb + (int64_t)t * p.q8_st + (int64_t)head * p.q8_sh + 8 * hi;
 #pragma unroll
-        for (int ks = 0; ks < KS_NOPE; ++ks) {
+        for (int ks = 0; ks < L::Q8_KS; ++ks) {
             const u32x2 c = *reinterpret_cast<const u32x2*>(q8p + 16 * ks);
             qf[ks] = u32x4{c[0], c[1], 0u, 0u};
         }
@@ -343,8 +352,8 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                                                    (int64_t)head * p.qsc_sh);
         const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head * p.q_sh + 8 * hi;
 #pragma unroll
-        for (int ks = KS_NOPE; ks < L::KS; ++ks)
-            qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * (ks - KS_NOPE));
+        for (int ks = L::Q8_KS; ks < L::KS; ++ks)
+            qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * (ks - L::Q8_KS));
     } else {
         const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head * p.q_sh + 8 * hi;
 #pragma unroll
@@ -454,7 +463,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         int32_t r[FP8 ? FP8_LPW : TILE / NWAVE];  // bf16: this wave's rows (uniform); fp8: per lane
         int32_t rope;                             // bf16: row of this lane's RoPE chunk
     };
-    const int my_loads = FP8 ? (wave < FP8_LOADS - NWAVE * (FP8_LPW - 1) ? FP8_LPW : FP8_LPW - 1) : L::LPW;
+    const int my_loads = FP8 ? (wave < L::LOADS - NWAVE * (FP8_LPW - 1) ? FP8_LPW : FP8_LPW - 1) : L::LPW;
     auto load_rows = [&](int ti) -> GatherRows {
         const LDS_AS int32_t* rows = s_rows + ti * TILE;
         const int ln = opaque(lane);
@@ -509,7 +518,16 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                 // < 32) into the slot's padding, so no lane is masked off.
                 const int k = wave + NWAVE * i;
                 const uint64_t row = (uint32_t)g.r[i];
-                if constexpr (L::MX) {
+                if constexpr (L::V4MX) {
+                    // NoPE (with its scales) or RoPE stream of the row's pool;
+                    // a row of the second (extend) pool carries the POOL2 tag
+                    const bool e2 = (g.r[i] & POOL2) != 0;
+                    const uint64_t r64 = (uint32_t)(g.r[i] & (POOL2 - 1));
+                    const unsigned char* src =
+                        k < 16 ? (e2 ? p.kv2 : p.kv) + r64 * p.kvn_st + 16 * (ln & 31)
+                               : (e2 ? p.kv2_ro : p.kv_ro) + r64 * p.kvr_st + 16 * (ln & 7);
+                    lds_dma16(src, RING + slot * RAW_STRIDE + 1024 * k);
+                } else if constexpr (L::MX) {
                     // one stream per load: base and row stride are wave-uniform
                     const unsigned char* src =
                         k < 16 ? p.kv + row * p.kvn_st + 16 * (ln & 31)
@@ -555,11 +573,24 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             const u32x2 codes = lds_ld<u32x2>(rr + 8 * ln);
             d.v[0] = codes[0];
             d.v[1] = codes[1];
-            if constexpr (L::MX)
+            if constexpr (L::V4MX) {
+                // lanes 0..55: codes 8l..8l+7 and the 8 scale bytes holding
+                // block l/4; lanes 56..63: RoPE values 8(l-56)..+7 (bf16)
+                if (ln >= 56) {
+                    const u32x4 rv = lds_ld<u32x4>(rb + MX_ROPE_OFF + 128 * r + 16 * (ln - 56));
+                    d.v = rv;
+                } else {
+                    const u32x2 sc8 = lds_ld<u32x2>(rr + DSA_MLA_V4_NOPE + 8 * (ln >> 5));
+                    d.v[2] = sc8[0];
+                    d.v[3] = sc8[1];
+                }
+            } else if constexpr (L::MX) {
                 d.v[2] = lds_ld<unsigned char>(rb + MX_SC_OFF + 16 * r + (ln >> 2));
-            else
+                d.v[3] = 0;
+            } else {
                 d.v[2] = __float_as_uint(lds_ld<float>(rr + FP8_SCALE_OFF + 4 * (ln >> 4)));
-            d.v[3] = 0;
+                d.v[3] = 0;
+            }
         } else {
             const int t8 = opaque(tid);
             if constexpr (L::MX)
@@ -573,7 +604,13 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         const int ln = opaque(lane);
         if (j < TILE / NWAVE) {
             const int r = wave + NWAVE * j;
-            if constexpr (L::MX) {
+            if constexpr (L::V4MX) {
+                const uint64_t sc8 = ((uint64_t)d.v[3] << 32) | d.v[2];
+                const unsigned e = (unsigned)(sc8 >> (8 * ((ln >> 2) & 7))) & 0xFFu;
+                const u32x4 cv = mx_to_bf16(d.v[0], d.v[1], e);
+                lds_st<u32x4>(tb + r * NOPE_STRIDE + 16 * (ln ^ nope_sw(r)), ln >= 56 ? d.v : cv);
+                return;
+            } else if constexpr (L::MX) {
                 lds_st<u32x4>(tb + r * NOPE_STRIDE + 16 * (ln ^ nope_sw(r)), mx_to_bf16(d.v[0], d.v[1], d.v[2]));
                 return;
             }
@@ -595,7 +632,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     };
     auto dequant = [&](lds_cptr rb, lds_ptr tb) {
 #pragma unroll
-        for (int j = 0; j < DEQ_PIECES; ++j) deq_store(tb, j, deq_load(rb, j));
+        for (int j = 0; j < (L::D512 ? DEQ_PIECES - 1 : DEQ_PIECES); ++j) deq_store(tb, j, deq_load(rb, j));
     };
 
     // ---- online softmax state (fixed reference max) ----
@@ -630,7 +667,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     } else if constexpr (L::MX) {
         // fp8 NoPE of Q -> bf16: dims 16ks + 8hi .. +7 lie in scale block ks / 2
 #pragma unroll
-        for (int ks = 0; ks < KS_NOPE; ++ks) {
+        for (int ks = 0; ks < L::Q8_KS; ++ks) {
             const unsigned e = (q_scales[ks >> 3] >> (8 * ((ks >> 1) & 3))) & 0xFFu;
             qf[ks] = mx_to_bf16(qf[ks][0], qf[ks][1], e);
         }
@@ -672,7 +709,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         // Software pipeline pinned with scheduling barriers: the K fragment of
         // k-step ks+KPF is read while MFMA ks runs; the gathers of tile
         // it+NPRE are issued between the MFMAs (one load every 4 k-steps).
-        constexpr int KPF = FP8 ? 4 : 6;     // fp8: register-bound at 4
+        constexpr int KPF = L::MX ? 3 : (FP8 ? 4 : 6);   // register-bound for the fp8 formats
         auto k_addr = [&](int ks) -> lds_cptr {
             return ks < KS_NOPE ? ((ks & 1) ? k_odd : k_even) + 64 * (ks >> 1)
                                 : k_rope + 16 * ((2 * (ks - KS_NOPE) + lhi) ^ rsw);
@@ -817,7 +854,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                 static_assert(DEQ_PIECES == 9, "dequant pieces vs MFMA groups");
                 __builtin_amdgcn_sched_barrier(0);
                 deq_store(nxt, 7, dq[1]);
-                deq_store(nxt, 8, deq_load(draw, 8));
+                if constexpr (!L::D512) deq_store(nxt, 8, deq_load(draw, 8));   // RoPE block
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -915,6 +952,9 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         constexpr int OUT_STRIDE = D_VO * 2 + 16;
         static_assert(32 * OUT_STRIDE <= TILE_BYTES, "O stage fits a tile buffer");
         __bf16* const orow = p.out + (int64_t)b * p.o_sb + (int64_t)t * p.o_st;
+        // per-lane stage offsets, computed here (not hoisted into the tile loop)
+        const int ln = opaque(lane);
+        const int st_w = opaque(r32 * OUT_STRIDE + 2 * d0);
         // 16-byte stores need 16-byte aligned rows; the API allows 8
         const bool o16 = ((p.o_sb | p.o_st | p.o_sh) & 7) == 0 && ((uintptr_t)p.out & 15) == 0;
 #pragma unroll
@@ -928,7 +968,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                     const f32x4 v4 = {a[4 * g] * inv[h], a[4 * g + 1] * inv[h], a[4 * g + 2] * inv[h],
                                       a[4 * g + 3] * inv[h]};
                     const bf16x4 bv = __builtin_convertvector(v4, bf16x4);
-                    lds_st<u32x2>(stg + r32 * OUT_STRIDE + 2 * (d0 + 32 * m + 8 * g), __builtin_bit_cast(u32x2, bv));
+                    lds_st<u32x2>(stg + st_w + 2 * (32 * m + 8 * g), __builtin_bit_cast(u32x2, bv));
                 }
             }
             __syncthreads();
@@ -936,8 +976,8 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 const int r = 8 * wave + k;
-                const u32x4 v = lds_ld<u32x4>(stg + r * OUT_STRIDE + 16 * lane);
-                __bf16* const dst = orow + (int64_t)(32 * h + r) * p.o_sh + 8 * lane;
+                const u32x4 v = lds_ld<u32x4>(stg + r * OUT_STRIDE + 16 * ln);
+                __bf16* const dst = orow + (int64_t)(32 * h + r) * p.o_sh + 8 * ln;
                 if (o16) {
                     *reinterpret_cast<u32x4*>(dst) = v;
                 } else {
@@ -1124,6 +1164,7 @@ int launch_fwd(const FwdParams& fp, int fmt, int B, int s_q, int ns, hipStream_t
     if (fmt == DSA_KV_BF16) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_BF16>, grid, block, 0, st, fp);
     else if (fmt == DSA_KV_FP8_656) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_FP8_656>, grid, block, 0, st, fp);
     else if (fmt == DSA_KV_MXFP8) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_MXFP8>, grid, block, 0, st, fp);
+    else if (fmt == DSA_KV_MXFP8_V4) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_MXFP8_V4>, grid, block, 0, st, fp);
     else hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_BF16_D512>, grid, block, 0, st, fp);
     return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_HIP;
 }
@@ -1202,7 +1243,7 @@ size_t mx_ws_bytes(const dsa_mla_decode_mxfp8_args* a, int ns) {
 
 extern "C" {
 
-int dsa_mla_abi_version(void) { return 4; }
+int dsa_mla_abi_version(void) { return 5; }
 
 const char* dsa_mla_strerror(int code) {
     switch (code) {
@@ -1454,6 +1495,54 @@ int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* a, void* stream) {
     fp.B = a->N; fp.s_q = 1; fp.topk = a->max_rows; fp.chunk = a->max_rows;
     fp.scale_log2 = a->softmax_scale * LOG2E;
     return launch_fwd(fp, DSA_KV_BF16_D512, a->N, 1, 1, (hipStream_t)stream);
+}
+int dsa_mla_prefill_v4_fp8(const dsa_mla_prefill_v4_fp8_args* a, void* stream) {
+    if (!a) return DSA_ERR_NULL_POINTER;
+    if (a->N < 0 || a->total_pages < 0 || a->total_tokens < 0 || a->max_rows < 0) return DSA_ERR_BAD_SHAPE;
+    if (a->H != HEADS || a->max_rows > MAX_CHUNK) return DSA_ERR_UNSUPPORTED;
+    if (a->N == 0) return DSA_OK;
+    if (!a->q_nope || !a->q_rope || !a->out || !a->kv_indptr_prefix || !a->kv_indices_prefix ||
+        !a->kv_indptr_extend || !a->kv_indices_extend)
+        return DSA_ERR_NULL_POINTER;
+    if ((a->total_pages > 0 && (!a->unified_kv_nope || !a->unified_kv_rope)) ||
+        (a->total_tokens > 0 && (!a->kv_nope || !a->kv_rope)))
+        return DSA_ERR_NULL_POINTER;
+    const int32_t b16[] = {a->stride_q_nope_n, a->stride_q_nope_h, a->stride_kv_nope_page};
+    for (int32_t v : b16) if (v < 0 || (v % 16)) return DSA_ERR_BAD_STRIDE;
+    if (a->stride_kv_nope_page < DSA_MLA_V4_NOPE_BYTES) return DSA_ERR_BAD_STRIDE;
+    const int32_t e8[] = {a->stride_q_rope_n, a->stride_q_rope_h, a->stride_kv_rope_page};
+    for (int32_t v : e8) if (v < 0 || (v % 8)) return DSA_ERR_BAD_STRIDE;
+    if (a->stride_o_n < 0 || a->stride_o_h < 0 || (a->stride_o_n % 4) || (a->stride_o_h % 4))
+        return DSA_ERR_BAD_STRIDE;
+    const void* ptrs[] = {a->q_nope, a->q_rope, a->unified_kv_nope, a->unified_kv_rope, a->kv_nope, a->kv_rope};
+    for (const void* q : ptrs) if ((uintptr_t)q & 15) return DSA_ERR_BAD_STRIDE;
+    if ((uintptr_t)a->out & 7) return DSA_ERR_BAD_STRIDE;
+    FwdParams fp{};
+    fp.q = (const __bf16*)a->q_rope;
+    fp.q_sb = a->stride_q_rope_n; fp.q_st = 0; fp.q_sh = a->stride_q_rope_h;
+    fp.q8 = (const unsigned char*)a->q_nope;
+    fp.q8_sb = a->stride_q_nope_n; fp.q8_st = 0; fp.q8_sh = a->stride_q_nope_h;
+    // the 14 scales of a Q head follow its 448 codes in the same stream row
+    fp.qsc = (const unsigned char*)a->q_nope + DSA_MLA_V4_NOPE;
+    fp.qsc_sb = fp.q8_sb; fp.qsc_st = 0; fp.qsc_sh = fp.q8_sh;
+    fp.kv = (const unsigned char*)a->unified_kv_nope;
+    fp.kv_ro = (const unsigned char*)a->unified_kv_rope;
+    fp.kv_total_rows = a->total_pages;
+    fp.kv2 = (const unsigned char*)a->kv_nope;
+    fp.kv2_ro = (const unsigned char*)a->kv_rope;
+    fp.kv2_rows = a->total_tokens;
+    fp.kvn_st = (uint32_t)a->stride_kv_nope_page;
+    fp.kvr_st = (uint32_t)a->stride_kv_rope_page * 2u;
+    fp.block_size = 1;
+    fp.ind_pre = a->kv_indptr_prefix; fp.idx_pre = a->kv_indices_prefix;
+    fp.ind_ext = a->kv_indptr_extend; fp.idx_ext = a->kv_indices_extend;
+    fp.attn_sink = a->attn_sink;
+    fp.out = (__bf16*)a->out;
+    fp.o_sb = a->stride_o_n; fp.o_st = 0; fp.o_sh = a->stride_o_h;
+    fp.lse = a->lse;
+    fp.B = a->N; fp.s_q = 1; fp.topk = a->max_rows; fp.chunk = a->max_rows;
+    fp.scale_log2 = a->softmax_scale * LOG2E;
+    return launch_fwd(fp, DSA_KV_MXFP8_V4, a->N, 1, 1, (hipStream_t)stream);
 }
 int dsa_kv_quantize_fp8(const void* src, int64_t src_stride, int64_t n_rows, void* dst, int64_t dst_total,
                         const int64_t* dst_rows, void* stream) {

@@ -400,3 +400,60 @@ def quantize_kv_fp8(src: torch.Tensor, dst: Optional[torch.Tensor] = None,
                                              dst.numel() // abi.FP8_ROW_BYTES, _ptr(dst_rows),
                                              _stream(stream)), "dsa_kv_quantize_fp8")
     return dst
+
+
+def mla_prefill_v4_fp8(q_nope: torch.Tensor, q_rope: torch.Tensor, unified_kv_nope: torch.Tensor,
+                       unified_kv_rope: torch.Tensor, kv_nope: torch.Tensor, kv_rope: torch.Tensor,
+                       attn_sink: Optional[torch.Tensor], kv_indptr_prefix: torch.Tensor,
+                       kv_indices_prefix: torch.Tensor, kv_indptr_extend: torch.Tensor,
+                       kv_indices_extend: torch.Tensor, softmax_scale: float,
+                       out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None, *,
+                       max_rows: Optional[int] = None, stream=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """DeepSeek-V4 sparse prefill on fp8 rows (opus_mla_v4_prefill_fp8_kargs form): every row and
+    Q head is a 512-byte NoPE stream row (448 e4m3 codes, 14 E8M0 scales, pad; uint8) plus 64 bf16
+    RoPE values; q_* [N, H, 512 | 64], pools [rows, 512 | 64].  Returns (out bf16 [N, H, 512],
+    lse fp32 [N, H])."""
+    for t, n in ((q_nope, "q_nope"), (unified_kv_nope, "unified_kv_nope"), (kv_nope, "kv_nope")):
+        _need(t, torch.uint8, n)
+        if t.shape[-1] != 512 or t.stride(-1) != 1:
+            raise ValueError(f"{n} must have 512-byte rows with a dense last dim")
+    for t, n in ((q_rope, "q_rope"), (unified_kv_rope, "unified_kv_rope"), (kv_rope, "kv_rope")):
+        _need(t, torch.bfloat16, n)
+        if t.shape[-1] != 64 or t.stride(-1) != 1:
+            raise ValueError(f"{n} must have 64 bf16 values per row with a dense last dim")
+    for t, n in ((kv_indptr_prefix, "kv_indptr_prefix"), (kv_indices_prefix, "kv_indices_prefix"),
+                 (kv_indptr_extend, "kv_indptr_extend"), (kv_indices_extend, "kv_indices_extend")):
+        _need(t, torch.int32, n)
+    if attn_sink is not None:
+        _need(attn_sink, torch.float32, "attn_sink")
+    N, H, _ = q_nope.shape
+    if tuple(q_rope.shape[:2]) != (N, H):
+        raise ValueError("q_nope and q_rope must cover the same [N, H]")
+    if unified_kv_nope.shape[0] != unified_kv_rope.shape[0] or kv_nope.shape[0] != kv_rope.shape[0]:
+        raise ValueError("each pool's nope and rope streams must have the same row count")
+    if unified_kv_nope.stride(0) != kv_nope.stride(0) or unified_kv_rope.stride(0) != kv_rope.stride(0):
+        raise ValueError("both pools must share the row strides (stride_kv_nope_page / _rope_page)")
+    if out is None:
+        out = torch.empty((N, H, abi.D_V4), dtype=torch.bfloat16, device=q_nope.device)
+    if lse is None:
+        lse = torch.empty((N, H), dtype=torch.float32, device=q_nope.device)
+    if max_rows is None:
+        max_rows = int(((kv_indptr_prefix[1:] - kv_indptr_prefix[:-1]) +
+                        (kv_indptr_extend[1:] - kv_indptr_extend[:-1])).max()) if N else 0
+    a = abi.PrefillV4Fp8Args()
+    a.q_nope, a.q_rope = _ptr(q_nope), _ptr(q_rope)
+    a.unified_kv_nope, a.unified_kv_rope = _ptr(unified_kv_nope), _ptr(unified_kv_rope)
+    a.kv_nope, a.kv_rope = _ptr(kv_nope), _ptr(kv_rope)
+    a.attn_sink, a.out, a.lse = _ptr(attn_sink), _ptr(out), _ptr(lse)
+    a.kv_indptr_prefix, a.kv_indices_prefix = _ptr(kv_indptr_prefix), _ptr(kv_indices_prefix)
+    a.kv_indptr_extend, a.kv_indices_extend = _ptr(kv_indptr_extend), _ptr(kv_indices_extend)
+    a.N, a.H = N, H
+    a.total_pages, a.total_tokens = unified_kv_nope.shape[0], kv_nope.shape[0]
+    a.stride_q_nope_n, a.stride_q_nope_h = q_nope.stride(0), q_nope.stride(1)
+    a.stride_q_rope_n, a.stride_q_rope_h = q_rope.stride(0), q_rope.stride(1)
+    a.stride_o_n, a.stride_o_h = out.stride(0), out.stride(1)
+    a.stride_kv_nope_page, a.stride_kv_rope_page = unified_kv_nope.stride(0), unified_kv_rope.stride(0)
+    a.max_rows = int(max_rows)
+    a.softmax_scale = float(softmax_scale)
+    check(load_library().dsa_mla_prefill_v4_fp8(ctypes.byref(a), _stream(stream)), "dsa_mla_prefill_v4_fp8")
+    return out, lse

@@ -20,8 +20,8 @@ import subprocess
 
 import numpy as np
 
-from opfoundry_amd.abi import (D_QK, D_V4, D_VO, DecodeArgs, KV_BF16, KV_FP8_656, MxArgs, PrefillArgs,
-                               PrefillV4Args)
+from opfoundry_amd.abi import (D_QK, D_V4, D_VO, V4_NOPE, DecodeArgs, KV_BF16, KV_FP8_656, MxArgs,
+                               PrefillArgs, PrefillV4Args, PrefillV4Fp8Args)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "_build", "libdsa_oracle.so")
@@ -61,6 +61,9 @@ def lib() -> ctypes.CDLL:
         L.oracle_mla_decode_mxfp8.argtypes = [ctypes.POINTER(MxArgs), ctypes.c_int]
         L.oracle_dequant_row_mxfp8.argtypes = [vp, vp, vp, vp]
         L.oracle_dequant_row_mxfp8.restype = None
+        L.oracle_mla_prefill_v4_fp8.argtypes = [ctypes.POINTER(PrefillV4Fp8Args), ctypes.c_int]
+        L.oracle_dequant_row_v4fp8.argtypes = [vp, vp, vp]
+        L.oracle_dequant_row_v4fp8.restype = None
         L.oracle_num_threads.argtypes = [ctypes.c_int]
         _LIB = L
     return _LIB
@@ -275,6 +278,50 @@ def mla_decode_mxfp8(q_nope, q_scale, q_rope, kv_nope, kv_scale, kv_rope, kv_ind
     return out, lse
 
 
+def dequant_rows_v4fp8(nope: np.ndarray, rope: np.ndarray) -> np.ndarray:
+    """V4 fp8 rows (uint8 [n,512]: 448 codes, 14 E8M0, pad; uint16 [n,64] bf16) -> fp32 [n,512]."""
+    nope = np.ascontiguousarray(nope, dtype=np.uint8).reshape(-1, 512)
+    rope = np.ascontiguousarray(rope, dtype=np.uint16).reshape(-1, 64)
+    out = np.zeros((nope.shape[0], D_V4), np.float32)
+    for r in range(nope.shape[0]):
+        lib().oracle_dequant_row_v4fp8(_p(nope[r]), _p(rope[r]), _p(out[r]))
+    return out
+
+
+def mla_prefill_v4_fp8(q_nope, q_rope, ukv_nope, ukv_rope, kv_nope, kv_rope, attn_sink, indptr_prefix,
+                       indices_prefix, indptr_extend, indices_extend, softmax_scale, *, num_threads=0):
+    """Host oracle of dsa_mla_prefill_v4_fp8 (dense streams): q_nope uint8 [N,H,512], q_rope uint16
+    [N,H,64], pools uint8 [rows,512] + uint16 [rows,64]; returns (O uint16 [N,H,512], LSE f32)."""
+    qn = np.ascontiguousarray(q_nope, dtype=np.uint8)
+    qr = np.ascontiguousarray(q_rope, dtype=np.uint16)
+    un = np.ascontiguousarray(ukv_nope, dtype=np.uint8).reshape(-1, 512)
+    ur = np.ascontiguousarray(ukv_rope, dtype=np.uint16).reshape(-1, 64)
+    xn = np.ascontiguousarray(kv_nope, dtype=np.uint8).reshape(-1, 512)
+    xr = np.ascontiguousarray(kv_rope, dtype=np.uint16).reshape(-1, 64)
+    sink = None if attn_sink is None else np.ascontiguousarray(attn_sink, dtype=np.float32)
+    ipp, idp = (np.ascontiguousarray(x, dtype=np.int32) for x in (indptr_prefix, indices_prefix))
+    ipe, ide = (np.ascontiguousarray(x, dtype=np.int32) for x in (indptr_extend, indices_extend))
+    N, H, _ = qn.shape
+    out = np.zeros((N, H, D_V4), np.uint16)
+    lse = np.zeros((N, H), np.float32)
+    a = PrefillV4Fp8Args()
+    a.q_nope, a.q_rope = _p(qn), _p(qr)
+    a.unified_kv_nope, a.unified_kv_rope, a.kv_nope, a.kv_rope = _p(un), _p(ur), _p(xn), _p(xr)
+    a.attn_sink, a.out, a.lse = _p(sink), _p(out), _p(lse)
+    a.kv_indptr_prefix, a.kv_indices_prefix = _p(ipp), _p(idp)
+    a.kv_indptr_extend, a.kv_indices_extend = _p(ipe), _p(ide)
+    a.N, a.H, a.total_pages, a.total_tokens = N, H, un.shape[0], xn.shape[0]
+    a.stride_q_nope_n, a.stride_q_nope_h = H * 512, 512
+    a.stride_q_rope_n, a.stride_q_rope_h = H * 64, 64
+    a.stride_o_n, a.stride_o_h = H * D_V4, D_V4
+    a.stride_kv_nope_page, a.stride_kv_rope_page = 512, 64
+    a.max_rows = int(max((ipp[1:] - ipp[:-1]).max(initial=0) + (ipe[1:] - ipe[:-1]).max(initial=0), 1))
+    a.softmax_scale = float(softmax_scale)
+    rc = lib().oracle_mla_prefill_v4_fp8(ctypes.byref(a), num_threads)
+    assert rc == 0
+    return out, lse
+
+
 def mla_prefill(q, kv, indices, sm_scale, *, causal=False, causal_offset=0, num_threads=0):
     """Host oracle of dsa_mla_prefill: q uint16 [N,H,576], kv uint16 [rows,576] or uint8
     [rows,656], indices int32 [N, topk]."""
@@ -326,6 +373,20 @@ def mxfp8_rows(rng: np.random.Generator, n: int):
     x = rng.standard_normal((n, 16, 32), dtype=np.float32) * np.ldexp(1.0, -e)[:, :, None].astype(np.float32)
     nope = fp8_encode(x.reshape(n, 512))
     return nope, (e + 127).astype(np.uint8), normal_bf16(rng, (n, 64))
+
+
+def v4fp8_rows(rng: np.random.Generator, n: int):
+    """V4 fp8 rows drawn as init_fp8_dsa_split (opus_attn/dsa_v4/common/mla_v4_host.cc:208-240):
+    14 blocks of 32 codes e4m3(N(0,1) * 2^-e), e in [0, 3], scale bytes e + 127 at 448..461,
+    the rest of the 512-byte row 0xFF; RoPE N(0,1) bf16.  Returns (nope uint8 [n,512],
+    rope uint16 [n,64])."""
+    nb = V4_NOPE // 32
+    e = rng.integers(0, 4, size=(n, nb))
+    x = rng.standard_normal((n, nb, 32), dtype=np.float32) * np.ldexp(1.0, -e)[:, :, None].astype(np.float32)
+    nope = np.full((n, 512), 0xFF, np.uint8)
+    nope[:, :V4_NOPE] = fp8_encode(x.reshape(n, V4_NOPE))
+    nope[:, V4_NOPE:V4_NOPE + nb] = (e + 127).astype(np.uint8)
+    return nope, normal_bf16(rng, (n, 64))
 
 
 def distinct_indices(rng: np.random.Generator, high: int, k: int) -> np.ndarray:

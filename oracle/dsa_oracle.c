@@ -22,6 +22,8 @@
  *     pools, attention sink, D=512) opus_attn/dsa_v4/common/mla_v4_host.cc:455-532
  *   - MXFP8 split-stream decode ... opus_attn/dsa_v32/common/host.cc:418-429 (dequant),
  *                                   :459-506 (CSR rows, count-based MTP causality)
+ *   - V4 fp8 prefill .............. opus_attn/dsa_v4/common/mla_v4_host.cc:443-453 (dequant),
+ *                                   :535-588 (prefix + extend rows, sink)
  *   - split combine ............... opus_attn/dsa_v32/common/mla_reduce.hpp:6-156
  *   - threading ................... opus_attn/dsa_v32/common/parallel.h:11-57
  * generalised to the top-k index form (-1 padding, seq_len and causal bounds,
@@ -541,4 +543,64 @@ int oracle_mla_decode_mxfp8(const dsa_mla_decode_mxfp8_args* a, int nthreads) {
     mx_ctx c = {a};
     const size_t scratch = (size_t)D_QK + a->max_kv_len + (size_t)a->max_kv_len * D_QK;
     return run_pool(mx_task, &c, (int64_t)a->B * a->s_q, scratch, nthreads);
+}
+
+/* ------------------------------------------------------- V4 fp8 prefill */
+
+/*
+ * decode_dsa_row_fp8 (opus_attn/dsa_v4/common/mla_v4_host.cc:443-453): value
+ * d < 448 = e4m3(nope[d]) * 2^(nope[448 + d / 32] - 127) (the scales follow
+ * the codes in the 512-byte stream row), values 448..511 the bf16 RoPE.
+ */
+void oracle_dequant_row_v4fp8(const uint8_t* nope, const uint16_t* rope, float* out) {
+    for (int d = 0; d < DSA_MLA_V4_NOPE; ++d)
+        out[d] = oracle_fp8_e4m3_decode(nope[d]) * ldexpf(1.0f, (int)nope[DSA_MLA_V4_NOPE + d / 32] - 127);
+    for (int j = 0; j < D_ROPE; ++j) out[DSA_MLA_V4_NOPE + j] = oracle_bf16_to_f32(rope[j]);
+}
+
+typedef struct {
+    const dsa_mla_prefill_v4_fp8_args* a;
+} prefill_v4_fp8_ctx;
+
+/*
+ * mla_v4_attention_ref_fp8 (mla_v4_host.cc:535-588): Q and every prefix then
+ * extend row dequantised to fp32, then mla_v4_attention_compute
+ * (:455-480) with softmax_scale as a parameter.  A row outside its pool is
+ * skipped (the reference reads it unchecked).
+ */
+static void prefill_v4_fp8_task(void* vctx, int64_t i, float* scratch) {
+    const dsa_mla_prefill_v4_fp8_args* a = ((const prefill_v4_fp8_ctx*)vctx)->a;
+    const int D = DSA_MLA_D_V4;
+    float* q = scratch;
+    float* scores = q + D;
+    float* kv = scores + a->max_rows;
+    int n = 0;
+    const int32_t pb = a->kv_indptr_prefix[i], pe = a->kv_indptr_prefix[i + 1];
+    const int32_t eb = a->kv_indptr_extend[i], ee = a->kv_indptr_extend[i + 1];
+    for (int pass = 0; pass < 2; ++pass) {
+        const int32_t* ind = pass == 0 ? a->kv_indices_prefix : a->kv_indices_extend;
+        const uint8_t* nope = (const uint8_t*)(pass == 0 ? a->unified_kv_nope : a->kv_nope);
+        const uint16_t* rope = (const uint16_t*)(pass == 0 ? a->unified_kv_rope : a->kv_rope);
+        const int32_t rows = pass == 0 ? a->total_pages : a->total_tokens;
+        for (int32_t k = pass == 0 ? pb : eb; k < (pass == 0 ? pe : ee) && n < a->max_rows; ++k) {
+            const int32_t j = ind[k];
+            if (j < 0 || j >= rows) continue;
+            oracle_dequant_row_v4fp8(nope + (int64_t)j * a->stride_kv_nope_page,
+                                     rope + (int64_t)j * a->stride_kv_rope_page, kv + (size_t)n * D);
+            ++n;
+        }
+    }
+    for (int h = 0; h < a->H; ++h) {
+        oracle_dequant_row_v4fp8((const uint8_t*)a->q_nope + i * a->stride_q_nope_n + h * a->stride_q_nope_h,
+                                 (const uint16_t*)a->q_rope + i * a->stride_q_rope_n + h * a->stride_q_rope_h, q);
+        uint16_t* o = (uint16_t*)a->out + i * a->stride_o_n + h * a->stride_o_h;
+        const float sink = a->attn_sink ? a->attn_sink[h] : -INFINITY;
+        attention_core_v4(q, kv, n, a->softmax_scale, sink, scores, o, a->lse ? a->lse + i * a->H + h : NULL);
+    }
+}
+
+int oracle_mla_prefill_v4_fp8(const dsa_mla_prefill_v4_fp8_args* a, int nthreads) {
+    prefill_v4_fp8_ctx c = {a};
+    const size_t scratch = (size_t)DSA_MLA_D_V4 + a->max_rows + (size_t)a->max_rows * DSA_MLA_D_V4;
+    return run_pool(prefill_v4_fp8_task, &c, a->N, scratch, nthreads);
 }

@@ -77,6 +77,7 @@ def _c_layout(struct: str, fields):
 @pytest.mark.parametrize("cls,name", [(abi.DecodeArgs, "dsa_mla_decode_args"),
                                       (abi.CsrArgs, "dsa_mla_decode_csr_args"),
                                       (abi.MxArgs, "dsa_mla_decode_mxfp8_args"),
+                                      (abi.PrefillV4Fp8Args, "dsa_mla_prefill_v4_fp8_args"),
                                       (abi.PrefillV4Args, "dsa_mla_prefill_v4_args"),
                                       (abi.PrefillArgs, "dsa_mla_prefill_args")])
 def test_struct_layout_matches_c(cls, name):
@@ -366,3 +367,41 @@ def test_combine_validation(lib, args, code):
 ])
 def test_quantize_validation(lib, args, code):
     assert lib.dsa_kv_quantize_fp8(*args) == code
+
+
+def _v4fp8_args(**kw):
+    a = abi.PrefillV4Fp8Args()
+    a.q_nope, a.q_rope = 0x1000, 0x2000
+    a.unified_kv_nope, a.unified_kv_rope, a.kv_nope, a.kv_rope = 0x3000, 0x4000, 0x5000, 0x6000
+    a.attn_sink, a.out, a.lse = 0x7000, 0x8000, 0x9000
+    a.kv_indptr_prefix, a.kv_indices_prefix = 0xA000, 0xB000
+    a.kv_indptr_extend, a.kv_indices_extend = 0xC000, 0xD000
+    a.N, a.H, a.total_pages, a.total_tokens = 16, 128, 1000, 100
+    a.stride_q_nope_n, a.stride_q_nope_h = 128 * 512, 512
+    a.stride_q_rope_n, a.stride_q_rope_h = 128 * 64, 64
+    a.stride_o_n, a.stride_o_h = 128 * 512, 512
+    a.stride_kv_nope_page, a.stride_kv_rope_page = 512, 64
+    a.max_rows = 640
+    a.softmax_scale = 0.04
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(H=64), -3), (dict(N=-1), -2), (dict(max_rows=-1), -2), (dict(total_pages=-1), -2),
+    (dict(max_rows=2049), -3),
+    (dict(q_nope=None), -1), (dict(q_rope=None), -1), (dict(out=None), -1),
+    (dict(unified_kv_nope=None), -1), (dict(kv_rope=None), -1), (dict(kv_indices_extend=None), -1),
+    (dict(stride_q_nope_h=520), -7), (dict(stride_kv_nope_page=496), -7), (dict(stride_kv_rope_page=60), -7),
+    (dict(stride_o_h=510), -7), (dict(kv_nope=0x5008), -7),
+])
+def test_prefill_v4_fp8_rejects_bad_arguments(lib, kw, code):
+    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(_v4fp8_args(**kw)), None) == code
+
+
+def test_prefill_v4_fp8_empty_is_a_no_op(lib):
+    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(_v4fp8_args(N=0)), None) == 0
+    # empty pools need no pool pointers
+    a = _v4fp8_args(N=0, total_pages=0, unified_kv_nope=None, unified_kv_rope=None)
+    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(a), None) == 0
