@@ -8,9 +8,10 @@ north-star target is quoted on) - fp8 656-byte KV rows, batch 128, MTP s_q = 2,
 128 heads, top-k 2048, seq_len 65536 paged at 64 rows, causal.  The JSON line
 also carries config 5 (bf16 sparse prefill, 8192 x 128 heads x top-k 2048) in
 TFLOP/s, the same decode on MXFP8 split streams (the reference's own -dtype fp8
-format, C3-shaped: B=128, s_q=2, 2048 rows per token), the dominant kernel's
-roofline for each, and the CPU oracle timed on a bounded sample of each
-workload on this host.
+format, C3-shaped: B=128, s_q=2, 2048 rows per token), the DeepSeek-V4
+prefill (bf16 and fp8 rows) at the reference harness's default shape, the
+dominant kernel's roofline for each, and the CPU oracle timed on a bounded
+sample of each workload on this host.
 
 Warm-up: by default at least 10 steps and 0.15 s of back-to-back calls per
 workload before the timed steps (the GPU takes tens of ms of sustained load to
@@ -52,6 +53,10 @@ CONFIGS = {
     # MXFP8 split streams (the reference's -dtype fp8 format), C3-shaped: the two tokens of an
     # MTP pair see 2047 and 2048 rows of their batch's CSR list (count-based causality)
     "mx": dict(kind="mxfp8", B=128, s_q=2, rows=2048),
+    # DeepSeek-V4 prefill at the reference harness's defaults (mla_v4_host.cc:779-830): N=4096
+    # queries, 1024 scattered prefix rows of 65536 pages plus a 128-row extend window, D=512
+    "v4": dict(kind="v4", N=4096, topk=1024, pages=65536, window=128, fp8=False),
+    "v4fp8": dict(kind="v4", N=4096, topk=1024, pages=65536, window=128, fp8=True),
 }
 NAMES = {
     "c1": "bf16 sparse MLA decode B=2 H=128 top-k 2048 (256 pad) flat KV 8192",
@@ -61,6 +66,9 @@ NAMES = {
     "c5": "bf16 sparse MLA prefill N=8192 H=128 top-k 2048 from [0,t]",
     "mx": ("MXFP8 split-stream sparse MLA decode (E8M0 per 32, CSR) B=128 s_q=2 (MTP) H=128, "
            "2048-row lists from a shuffled page table"),
+    "v4": "DeepSeek-V4 bf16 prefill N=4096 H=128 D=512, top-k 1024 of 65536 pages + window 128, sink",
+    "v4fp8": ("DeepSeek-V4 fp8 prefill (448 e4m3 + 14 E8M0 | 64 bf16) N=4096 H=128, top-k 1024 of "
+              "65536 pages + window 128, sink"),
 }
 
 
@@ -238,6 +246,120 @@ def cpu_baseline_mx(m, sample_batches):
     return dict(value=dt * B / nb * 1e6, unit="us/step", cores=nt, kind="port",
                 sample=f"{nb} of {B} batches ({nb * s_q} query tokens, all 128 heads), {dt:.2f} s "
                        f"measured, scaled x{B / nb:.1f} to one step")
+
+
+def make_v4(cfg, dev, seed=2051):
+    """V4 prefill inputs as the reference harness draws them (mla_v4_host.cc:208-290): per query
+    `topk` distinct scattered prefix pages and its last min(i + 1, window) extend rows; values
+    N(0,1) (bf16), or init_fp8_dsa_split rows (fp8: 14 blocks of e4m3(N(0,1) * 2^-e), e in
+    [0, 3], scale bytes e + 127, pad 0xFF; RoPE N(0,1) bf16); per-head sink N(0,1)."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    N, topk, pages, window = cfg["N"], cfg["topk"], cfg["pages"], cfg["window"]
+    idp = torch.empty((N, topk), dtype=torch.int32, device=dev)
+    for r0 in range(0, N, 256):
+        n = min(256, N - r0)
+        idp[r0:r0 + n] = torch.rand((n, pages), generator=g, device=dev).argsort(dim=1)[:, :topk].to(torch.int32)
+    ipp = torch.arange(N + 1, device=dev, dtype=torch.int32) * topk
+    ne = torch.clamp(torch.arange(N, device=dev) + 1, max=window)
+    ipe = torch.zeros(N + 1, dtype=torch.int32, device=dev)
+    ipe[1:] = torch.cumsum(ne, 0).to(torch.int32)
+    qi = torch.repeat_interleave(torch.arange(N, device=dev), ne)
+    ide = (qi - (ipe[:-1].long()[qi] + ne[qi] - 1 - torch.arange(qi.numel(), device=dev))).to(torch.int32)
+
+    def rows(n):
+        if not cfg["fp8"]:
+            return torch.randn((n, 512), generator=g, device=dev).to(torch.bfloat16)
+        e = torch.randint(0, 4, (n, 14), generator=g, device=dev)
+        x = torch.randn((n, 14, 32), generator=g, device=dev) * torch.exp2(-e.float())[:, :, None]
+        nope = torch.full((n, 512), 0xFF, dtype=torch.uint8, device=dev)
+        nope[:, :448] = x.reshape(n, 448).to(torch.float8_e4m3fn).view(torch.uint8)
+        nope[:, 448:462] = (e + 127).to(torch.uint8)
+        return nope, torch.randn((n, 64), generator=g, device=dev).to(torch.bfloat16)
+
+    q, ukv, xkv = rows(N * H), rows(pages), rows(N)
+    if cfg["fp8"]:
+        q = (q[0].view(N, H, 512), q[1].view(N, H, 64))
+    else:
+        q = q.view(N, H, 512)
+    sink = torch.randn((H,), generator=g, device=dev)
+    torch.cuda.synchronize()
+    return dict(q=q, ukv=ukv, xkv=xkv, sink=sink, lists=(ipp, idp.view(-1), ipe, ide), fp8=cfg["fp8"],
+                rows=N * topk + int(ne.sum()), N=N)
+
+
+def v4_step(v, dev):
+    """(step, buffers) for one V4 prefill call through the C ABI (arguments built once)."""
+    import ctypes
+    import torch
+    from opfoundry_amd import abi
+    from opfoundry_amd.abi import check, load_library
+    N = v["N"]
+    out = torch.empty((N, H, 512), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((N, H), dtype=torch.float32, device=dev)
+    ipp, idp, ipe, ide = v["lists"]
+    mr = int(((ipp[1:] - ipp[:-1]) + (ipe[1:] - ipe[:-1])).max())
+    if v["fp8"]:
+        a = abi.PrefillV4Fp8Args()
+        a.q_nope, a.q_rope = v["q"][0].data_ptr(), v["q"][1].data_ptr()
+        a.unified_kv_nope, a.unified_kv_rope = v["ukv"][0].data_ptr(), v["ukv"][1].data_ptr()
+        a.kv_nope, a.kv_rope = v["xkv"][0].data_ptr(), v["xkv"][1].data_ptr()
+        a.total_pages, a.total_tokens = v["ukv"][0].shape[0], v["xkv"][0].shape[0]
+        a.stride_q_nope_n, a.stride_q_nope_h = H * 512, 512
+        a.stride_q_rope_n, a.stride_q_rope_h = H * 64, 64
+        a.stride_o_n, a.stride_o_h = H * 512, 512
+        a.stride_kv_nope_page, a.stride_kv_rope_page = 512, 64
+        fn, name = load_library().dsa_mla_prefill_v4_fp8, "dsa_mla_prefill_v4_fp8"
+    else:
+        a = abi.PrefillV4Args()
+        a.q, a.unified_kv, a.kv = v["q"].data_ptr(), v["ukv"].data_ptr(), v["xkv"].data_ptr()
+        a.D = 512
+        a.total_pages, a.total_tokens = v["ukv"].shape[0], v["xkv"].shape[0]
+        a.stride_qo_n, a.stride_qo_h = H * 512, 512
+        a.stride_kv_page = 512
+        fn, name = load_library().dsa_mla_prefill_v4, "dsa_mla_prefill_v4"
+    a.attn_sink, a.out, a.lse = v["sink"].data_ptr(), out.data_ptr(), lse.data_ptr()
+    a.kv_indptr_prefix, a.kv_indices_prefix = ipp.data_ptr(), idp.data_ptr()
+    a.kv_indptr_extend, a.kv_indices_extend = ipe.data_ptr(), ide.data_ptr()
+    a.N, a.H, a.max_rows = N, H, mr
+    a.softmax_scale = 1.0 / math.sqrt(512.0)
+    ap = ctypes.byref(a)
+    st = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        rc = fn(ap, st)
+        if rc:
+            check(rc, name)
+    return step, (out, lse, a)
+
+
+def cpu_baseline_v4(v, sample):
+    """The C oracle on the first `sample` queries of the V4 step, scaled to the whole step."""
+    import numpy as np
+    import torch
+    import oracle
+    N = v["N"]
+    n = min(sample, N)
+    ipp, idp, ipe, ide = (x.cpu().numpy() for x in v["lists"])
+    lists = (ipp[:n + 1], idp[:ipp[n]], ipe[:n + 1], ide[:ipe[n]])
+    b16 = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+    sink = v["sink"].cpu().numpy()
+    scale = 1.0 / math.sqrt(512.0)
+    nt = oracle.num_threads()
+    if v["fp8"]:
+        args = (v["q"][0][:n].cpu().numpy(), b16(v["q"][1][:n]), v["ukv"][0].cpu().numpy(), b16(v["ukv"][1]),
+                v["xkv"][0].cpu().numpy(), b16(v["xkv"][1]), sink, *lists, scale)
+        t0 = time.perf_counter()
+        oracle.mla_prefill_v4_fp8(*args, num_threads=nt)
+    else:
+        args = (b16(v["q"][:n]), b16(v["ukv"]), b16(v["xkv"]), sink, *lists, scale)
+        t0 = time.perf_counter()
+        oracle.mla_prefill_v4(*args, num_threads=nt)
+    dt = time.perf_counter() - t0
+    rows = int(ipp[n] + ipe[n])
+    return dict(value=4.0 * H * rows * 512 / dt / 1e12, unit="TFLOP/s", cores=nt, kind="port",
+                sample=f"{n} of {N} queries ({rows} rows), {dt:.2f} s")
 
 
 def count_valid(d) -> int:
@@ -428,6 +550,9 @@ def main():
                     help="decode workload of the JSON line (c5 only with --kernel-only)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-mx", action="store_true")
+    ap.add_argument("--no-v4", action="store_true")
+    ap.add_argument("--cpu-v4-sample", type=int, default=128,
+                    help="V4 prefill queries the CPU oracle runs")
     ap.add_argument("--cpu-mx-sample", type=int, default=64,
                     help="batches of the mx step (both MTP tokens) the CPU oracle runs")
     ap.add_argument("--no-cpu", action="store_true")
@@ -459,6 +584,14 @@ def main():
         ms = time_steps(lambda: dst.copy_(src), args.steps, args.warmup)
         print(json.dumps({"copy_bytes": n, "ms_per_copy": ms,
                           "GBps_read_plus_write": 2 * n / (ms * 1e-3) / 1e9}))
+        return
+    if cfg["kind"] == "v4":
+        if not args.kernel_only:
+            ap.error("--config v4 / v4fp8 are reported inside the default JSON line; use them with --kernel-only")
+        log(f"building {args.config} inputs")
+        v = make_v4(cfg, dev)
+        ms = time_steps(v4_step(v, dev)[0], args.steps, args.warmup)
+        print(json.dumps({"config": args.config, "ms_per_step": ms}))
         return
     if cfg["kind"] == "mxfp8":
         if not args.kernel_only:
@@ -574,6 +707,31 @@ def main():
             res["mxfp8"]["cpu_baseline"] = cpu_baseline_mx(m, args.cpu_mx_sample)
         del m
         torch.cuda.empty_cache()
+
+    if not args.no_v4:
+        res["v4_prefill"] = {}
+        for name in ("v4", "v4fp8"):
+            log(f"building {name} inputs")
+            v = make_v4(CONFIGS[name], dev)
+            vstep, keep = v4_step(v, dev)
+            vsteps = max(5, args.steps // 5)
+            vms = time_steps(vstep, vsteps, args.warmup)    # one kernel per step
+            vfl = 4.0 * H * v["rows"] * 512                   # the reference's count (mla_v4_host.cc:358)
+            leg = {"workload": f"{name}: {NAMES[name]}", "ms_per_step": round(vms, 4),
+                   "tflops": round(vfl / (vms * 1e-3) / 1e12, 1), "rows": v["rows"],
+                   "roofline": {"bound": "mfma", "achieved": round(vfl / (vms * 1e-3) / 1e12, 1),
+                                "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                "frac": round(vfl / (vms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                                "traffic": profiled_traffic(f"dsa_mla_fwd_{name}_traffic.txt"),
+                                "kernel": "dsa_mla_fwd_kernel<mxfp8_v4>" if v["fp8"] else "dsa_mla_fwd_kernel<bf16_d512>",
+                                "kernel_avg_us": round(vms * 1e3, 1)}}
+            del keep
+            if not args.no_cpu:
+                log(f"CPU baseline (oracle) on a {name} sample")
+                leg["cpu_baseline"] = cpu_baseline_v4(v, args.cpu_v4_sample)
+            res["v4_prefill"][name] = leg
+            del v, vstep
+            torch.cuda.empty_cache()
 
     if not args.no_prefill:
         log("building c5 prefill inputs")

@@ -520,12 +520,21 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                 const uint64_t row = (uint32_t)g.r[i];
                 if constexpr (L::V4MX) {
                     // NoPE (with its scales) or RoPE stream of the row's pool;
-                    // a row of the second (extend) pool carries the POOL2 tag
+                    // a row of the second (extend) pool carries the POOL2 tag.
+                    // The pool pointers pass through registers the compiler
+                    // cannot trace to the argument block: a per-lane choice
+                    // between two argument fields otherwise becomes a per-lane
+                    // load of the field, whose vmcnt wait drains the gathers.
+                    const unsigned char* n0 = p.kv;
+                    const unsigned char* n1 = p.kv2;
+                    const unsigned char* q0 = p.kv_ro;
+                    const unsigned char* q1 = p.kv2_ro;
+                    asm("" : "+s"(n0), "+s"(n1), "+s"(q0), "+s"(q1));
                     const bool e2 = (g.r[i] & POOL2) != 0;
                     const uint64_t r64 = (uint32_t)(g.r[i] & (POOL2 - 1));
                     const unsigned char* src =
-                        k < 16 ? (e2 ? p.kv2 : p.kv) + r64 * p.kvn_st + 16 * (ln & 31)
-                               : (e2 ? p.kv2_ro : p.kv_ro) + r64 * p.kvr_st + 16 * (ln & 7);
+                        k < 16 ? (e2 ? n1 : n0) + r64 * p.kvn_st + 16 * (ln & 31)
+                               : (e2 ? q1 : q0) + r64 * p.kvr_st + 16 * (ln & 7);
                     lds_dma16(src, RING + slot * RAW_STRIDE + 1024 * k);
                 } else if constexpr (L::MX) {
                     // one stream per load: base and row stride are wave-uniform
@@ -570,21 +579,21 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         if (j < TILE / NWAVE) {
             const int r = wave + NWAVE * j;
             const lds_cptr rr = rb + r * (L::MX ? D_NOPE : FP8_ROW);
+            if constexpr (L::V4MX) {
+                // lanes 0..55: codes 8l..8l+7, then the 8 scale bytes holding
+                // block l/4; lanes 56..63: RoPE values 8(l-56)..+7 (bf16) in
+                // two halves.  Same two loads on every lane: no branch.
+                const bool rp = ln >= 56;
+                const lds_cptr ra = rb + MX_ROPE_OFF + 128 * r + 16 * (ln & 7);
+                const u32x2 lo = lds_ld<u32x2>(rp ? ra : rr + 8 * ln);
+                const u32x2 hi8 = lds_ld<u32x2>(rp ? ra + 8 : rr + DSA_MLA_V4_NOPE + 8 * (ln >> 5));
+                d.v = u32x4{lo[0], lo[1], hi8[0], hi8[1]};
+                return d;
+            }
             const u32x2 codes = lds_ld<u32x2>(rr + 8 * ln);
             d.v[0] = codes[0];
             d.v[1] = codes[1];
-            if constexpr (L::V4MX) {
-                // lanes 0..55: codes 8l..8l+7 and the 8 scale bytes holding
-                // block l/4; lanes 56..63: RoPE values 8(l-56)..+7 (bf16)
-                if (ln >= 56) {
-                    const u32x4 rv = lds_ld<u32x4>(rb + MX_ROPE_OFF + 128 * r + 16 * (ln - 56));
-                    d.v = rv;
-                } else {
-                    const u32x2 sc8 = lds_ld<u32x2>(rr + DSA_MLA_V4_NOPE + 8 * (ln >> 5));
-                    d.v[2] = sc8[0];
-                    d.v[3] = sc8[1];
-                }
-            } else if constexpr (L::MX) {
+            if constexpr (L::MX) {
                 d.v[2] = lds_ld<unsigned char>(rb + MX_SC_OFF + 16 * r + (ln >> 2));
                 d.v[3] = 0;
             } else {
