@@ -123,3 +123,36 @@ def test_c5_prefill_full_size(dev):
     e = assert_parity(bits(out[sel]), lse[sel].cpu().numpy(), o_ref, l_ref, "C5 full size")
     print(f"[case] C5 full size: {len(sel)} sampled queries, max|dO|={e[0]:.3e} "
           f"max rel dLSE={e[1]:.3e}", flush=True)
+
+
+@pytest.mark.parametrize("name", ["v4", "v4fp8"])
+def test_v4_prefill_full_size(dev, name):
+    """The V4 bench workloads (the reference harness's defaults: N=4096, top-k 1024 of 65536
+    pages, window 128, sink): sampled queries against the oracle."""
+    print(f"[case] {name} full size: N=4096, top-k 1024 of 65536 pages, window 128", flush=True)
+    v = bench.make_v4(bench.CONFIGS[name], dev)
+    step, keep = bench.v4_step(v, dev)
+    step()
+    torch.cuda.synchronize()
+    out, lse = keep[0], keep[1]
+    assert torch.isfinite(lse).all() and torch.isfinite(out.float()).all()
+    ipp, idp, ipe, ide = (x.cpu().numpy() for x in v["lists"])
+    sel = [0, 1, 127, 128, 2000, 4095]
+    lists = [[0], [], [0], []]
+    for i in sel:
+        lists[1] += list(idp[ipp[i]:ipp[i + 1]])
+        lists[3] += list(ide[ipe[i]:ipe[i + 1]])
+        lists[0].append(len(lists[1]))
+        lists[2].append(len(lists[3]))
+    lists = [np.array(x, np.int32) for x in lists]
+    b16 = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+    sink = v["sink"].cpu().numpy()
+    scale = 1.0 / np.sqrt(512.0)
+    if v["fp8"]:
+        o_ref, l_ref = oracle.mla_prefill_v4_fp8(v["q"][0][sel].cpu().numpy(), b16(v["q"][1][sel]),
+                                                 v["ukv"][0].cpu().numpy(), b16(v["ukv"][1]),
+                                                 v["xkv"][0].cpu().numpy(), b16(v["xkv"][1]), sink, *lists, scale)
+    else:
+        o_ref, l_ref = oracle.mla_prefill_v4(b16(v["q"][sel]), b16(v["ukv"]), b16(v["xkv"]), sink, *lists, scale)
+    e = assert_parity(bits(out[sel]), lse[sel].cpu().numpy(), o_ref, l_ref, f"{name} full size")
+    print(f"[case] {name}: {len(sel)} sampled queries, max|dO|={e[0]:.3e} max rel dLSE={e[1]:.3e}", flush=True)
