@@ -660,13 +660,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // dims across the waves, so each gathered V value is read by one wave).
     f32x16 o[D_VO / 32];
     float m_ref = 0.0f, l_lane = 0.0f, s_max = -INFINITY;
-    constexpr int NPRE = FP8 ? 3 : 2;       // tiles in flight before the loop
-    GatherRows gnext;
-#pragma unroll
-    for (int s = 0; s < NPRE; ++s)
-        if (s < ntiles) issue_rows(load_rows(s), s);
-    if (NPRE < ntiles) gnext = load_rows(NPRE);
-
+    // Q (and the index loads) complete before the first gathers are issued:
+    // inside the loop the only vector-memory loads are the LDS-DMA gathers,
+    // counted explicitly, and the first tile waits for its own rows alone.
+    wait_vm<0>();
     if constexpr (L::F16) {
         // the NoPE part of Q is converted to fp16 for the fp16 MFMAs
 #pragma unroll
@@ -681,9 +678,12 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             qf[ks] = mx_to_bf16(qf[ks][0], qf[ks][1], e);
         }
     }
-    // Q (and the first gathers) complete before the tile loop: inside the loop
-    // the only vector-memory loads are the LDS-DMA gathers counted explicitly.
-    wait_vm<0>();
+    constexpr int NPRE = FP8 ? 3 : 2;       // tiles in flight before the loop
+    GatherRows gnext;
+#pragma unroll
+    for (int s = 0; s < NPRE; ++s)
+        if (s < ntiles) issue_rows(load_rows(s), s);
+    if (NPRE < ntiles) gnext = load_rows(NPRE);
 
     // P values -> MFMA operand (fp16 for the 656-B cache, else bf16)
     auto to_p = [&](const float* e) -> u32x4 {
