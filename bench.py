@@ -65,7 +65,7 @@ NAMES = {
     "c4": "bf16 split-top-k decode B=4 H=128 top-k<=2048 seq U[1024,131072] 8 splits + combine",
     "c5": "bf16 sparse MLA prefill N=8192 H=128 top-k 2048 from [0,t]",
     "mx": ("MXFP8 split-stream sparse MLA decode (E8M0 per 32, CSR) B=128 s_q=2 (MTP) H=128, "
-           "2048-row lists from a shuffled page table"),
+           "2048-row lists from a shuffled page table (2 disjoint index sets alternate step by step)"),
     "v4": "DeepSeek-V4 bf16 prefill N=4096 H=128 D=512, top-k 1024 of 65536 pages + window 128, sink",
     "v4fp8": ("DeepSeek-V4 fp8 prefill (448 e4m3 + 14 E8M0 | 64 bf16) N=4096 H=128, top-k 1024 of "
               "65536 pages + window 128, sink"),
@@ -164,10 +164,16 @@ def prefill_step(p, dev):
     return prepared_prefill(a, ws), (pout, plse, a, ws)
 
 
+MX_SETS = 2
+
+
 def make_mx(cfg, dev, seed=2041):
     """MXFP8 split streams drawn as init_fp8_mla_split (opus_attn/dsa_v32/common/host.cc:207-237):
     per 32-value block e in [0, 3], scale byte e + 127, codes e4m3(N(0,1) * 2^-e); RoPE N(0,1)
-    bf16.  The page table is a shuffled permutation of all rows (host.cc:239-262)."""
+    bf16.  The page table is a shuffled permutation of all rows (host.cc:239-262).  For HBM
+    honesty the pool holds MX_SETS times the rows one step references, and MX_SETS disjoint
+    index sets alternate step by step: consecutive steps touch MX_SETS x 172 MB of distinct rows,
+    more than the 256 MB MALL holds (one set alone would stay cache-resident)."""
     import torch
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
@@ -180,27 +186,31 @@ def make_mx(cfg, dev, seed=2041):
         rope = torch.randn((n, 64), generator=g, device=dev).to(torch.bfloat16)
         return nope, (e + 127).to(torch.uint8), rope
 
-    total = B * L
+    total = MX_SETS * B * L
     kv = streams(total)
     qn, qs, qr = streams(B * s_q * H)
     q = (qn.view(B * s_q, H, 512), qs.view(B * s_q, H, 16), qr.view(B * s_q, H, 64))
     indptr = (torch.arange(B + 1, device=dev, dtype=torch.int32) * L)
-    indices = torch.randperm(total, generator=g, device=dev).to(torch.int32)
+    perm = torch.randperm(total, generator=g, device=dev).to(torch.int32)
+    sets = [perm[i * B * L:(i + 1) * B * L].contiguous() for i in range(MX_SETS)]
     torch.cuda.synchronize()
-    return dict(q=q, kv=kv, indptr=indptr, indices=indices, s_q=s_q, L=L)
+    return dict(q=q, kv=kv, indptr=indptr, indices=sets[0], sets=sets, s_q=s_q, L=L)
 
 
-def prepared_mx(a, ws):
+def prepared_mx(args, ws):
+    """Steps alternate over the prepared argument blocks (one per index set)."""
     import ctypes
     import torch
     from opfoundry_amd.abi import check, load_library
     fn = load_library().dsa_mla_decode_mxfp8
-    ap = ctypes.byref(a)
+    aps = [ctypes.byref(a) for a in args]
+    turn = [0]
     wp, wb = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
     st = torch.cuda.current_stream().cuda_stream
 
     def step():
-        rc = fn(ap, wp, wb, st)
+        rc = fn(aps[turn[0]], wp, wb, st)
+        turn[0] = (turn[0] + 1) % len(aps)
         if rc:
             check(rc, "dsa_mla_decode_mxfp8")
     return step
@@ -215,13 +225,14 @@ def mx_step(m, dev):
     T = m["q"][0].shape[0]
     out = torch.empty((T, H, D_VO), dtype=torch.bfloat16, device=dev)
     lse = torch.empty((T, H), dtype=torch.float32, device=dev)
-    a = dsa.make_decode_mxfp8_args(*m["q"], *m["kv"], m["indptr"], m["indices"], SM_SCALE, out, lse,
-                                   s_q=m["s_q"], max_kv_len=m["L"])
+    args = [dsa.make_decode_mxfp8_args(*m["q"], *m["kv"], m["indptr"], ix, SM_SCALE, out, lse,
+                                       s_q=m["s_q"], max_kv_len=m["L"]) for ix in m["sets"]]
+    a = args[0]
     n = ctypes.c_size_t(0)
     check(load_library().dsa_mla_decode_mxfp8_workspace_size(ctypes.byref(a), ctypes.byref(n)),
           "dsa_mla_decode_mxfp8_workspace_size")
     ws = torch.empty(n.value, dtype=torch.uint8, device=dev) if n.value else None
-    return prepared_mx(a, ws), (out, lse, a, ws), (1 if not n.value else None)
+    return prepared_mx(args, ws), (out, lse, args, ws), (1 if not n.value else None)
 
 
 def cpu_baseline_mx(m, sample_batches):
@@ -360,6 +371,27 @@ def cpu_baseline_v4(v, sample):
     rows = int(ipp[n] + ipe[n])
     return dict(value=4.0 * H * rows * 512 / dt / 1e12, unit="TFLOP/s", cores=nt, kind="port",
                 sample=f"{n} of {N} queries ({rows} rows), {dt:.2f} s")
+
+
+def measured_peaks(dev):
+    """Achievable rates on this GPU, beside the spec peaks: a STREAM-like 2 GiB device copy
+    (read + write bytes / time) and a large dense bf16 GEMM through torch (hipBLASLt)."""
+    import torch
+    n = 2 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    copy_ms = time_steps(lambda: dst.copy_(src), 10, 5)
+    del src, dst
+    m = 8192
+    a = torch.randn((m, m), device=dev).to(torch.bfloat16)
+    b = torch.randn((m, m), device=dev).to(torch.bfloat16)
+    c = torch.empty((m, m), device=dev, dtype=torch.bfloat16)
+    gemm_ms = time_steps(lambda: torch.matmul(a, b, out=c), 10, 5)
+    del a, b, c
+    torch.cuda.empty_cache()
+    return {"hbm_copy_GBps": round(2 * n / (copy_ms * 1e-3) / 1e9, 1),
+            "bf16_gemm_TFLOPs": round(2 * m ** 3 / (gemm_ms * 1e-3) / 1e12, 1),
+            "how": "device copy of 2 GiB (read + write bytes); torch.matmul bf16 8192^3"}
 
 
 def count_valid(d) -> int:
@@ -551,6 +583,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-mx", action="store_true")
     ap.add_argument("--no-v4", action="store_true")
+    ap.add_argument("--no-peaks", action="store_true")
     ap.add_argument("--cpu-v4-sample", type=int, default=128,
                     help="V4 prefill queries the CPU oracle runs")
     ap.add_argument("--cpu-mx-sample", type=int, default=64,
@@ -753,6 +786,18 @@ def main():
                                        "kernel_avg_us": round(pk_ms * 1e3, 1)}}
         if not args.no_cpu:
             res["prefill"]["cpu_baseline"] = cpu_baseline_prefill(p, args.cpu_prefill_sample, pV)
+    if not args.no_peaks:
+        log("measured peaks (copy, bf16 GEMM)")
+        pk = measured_peaks(dev)
+        res["measured_peaks"] = pk
+        # fractions against the achievable rates beside the spec ones
+        res["roofline"]["frac_measured"] = round(res["roofline"]["achieved"] / pk["hbm_copy_GBps"], 4)
+        if "mxfp8" in res:
+            r = res["mxfp8"]["roofline"]
+            r["frac_measured"] = round(r["achieved"] / pk["hbm_copy_GBps"], 4)
+        for leg in [res.get("prefill")] + list(res.get("v4_prefill", {}).values()):
+            if leg:
+                leg["roofline"]["frac_measured"] = round(leg["roofline"]["achieved"] / pk["bf16_gemm_TFLOPs"], 4)
     print(json.dumps(res))
 
 
