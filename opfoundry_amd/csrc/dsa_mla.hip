@@ -7,16 +7,21 @@
 // and compacted (invalid entries dropped), then processed in tiles of 32 rows:
 //   gather   16-byte LDS-DMA loads (global_load_lds_dwordx4) of whole rows,
 //            issued 2 (bf16) / 3 (fp8) tiles ahead of use
-//   dequant  fp8 rows only: cooperative e4m3 -> fp16 conversion of the next
-//            tile (v_cvt_scalef32_pk_f16_fp8 applies the power-of-two part of
-//            the per-128 scale, v_pk_mul_f16 its mantissa), overlapped with the
-//            QK^T MFMAs of the current tile
-//   QK^T     S^T[32 rows x 32 heads] with 32x32x16 MFMAs (bf16, or fp16 for the
-//            fp8 cache), Q held in registers, two accumulator chains
+//   dequant  fp8 rows only: cooperative conversion of the next tile into a
+//            16-bit tile buffer (656-B rows: v_cvt_scalef32_pk_f16_fp8 applies
+//            the power-of-two part of the per-128 scale, v_pk_mul_f16 its
+//            mantissa; MXFP8 rows: exact bf16), between the PV MFMAs
+//   QK^T     each wave: S^T[32 rows x its 32 heads] with 32x32x16 MFMAs (bf16,
+//            or fp16 for the 656-B cache), Q held in registers
 //   softmax  exp2 of the scores against a fixed per-head reference (the first
 //            tile's maximum): the O accumulators are never rescaled in the loop
-//   PV       O^T[512 x 32 heads] += V^T P^T, V^T read with ds_read_b64_tr_b16,
-//            P^T taken straight from the score registers
+//   PV       each wave: O^T[its 128 dims x 128 heads] += V^T P^T, V^T read
+//            with ds_read_b64_tr_b16, P exchanged between the waves in LDS
+// One wave per SIMD: the wave's VALU instructions do not overlap its MFMAs, so
+// the tile loops keep the non-MFMA instruction count low (one QK^T chain,
+// branches rather than selects for the last-tile masks, scalar row addresses).
+// bf16 caches run a software-pipelined loop (QK^T of tile t+1 and the softmax
+// numerators of tile t+1 within PV of tile t, one barrier per tile).
 // The structure follows the reference's one-workgroup-per-work-item decode
 // (opus_attn/dsa_v32/gfx950/mla_decode_a16w16_32mxt_32nx1_template.hpp:916-1132)
 // but is written from scratch for stock hipcc: no OPUS, no pinned registers,
@@ -26,6 +31,7 @@
 #include <stdint.h>
 #include <float.h>
 #include <algorithm>
+#include <type_traits>
 
 #include "../../include/dsa_mla.h"
 
@@ -179,6 +185,19 @@ __device__ __forceinline__ void lds_dma16(const void* gsrc, lds_ptr lds_wave_bas
         : "memory", "m0");
 }
 
+// The same load for a wave-uniform source row: 64-bit base in SGPRs plus a
+// 32-bit per-lane byte offset (no per-lane 64-bit address arithmetic).
+__device__ __forceinline__ void lds_dma16_s(const void* sbase, unsigned voff, lds_ptr lds_wave_base) {
+    const unsigned m0v = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_wave_base);
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2"
+        :
+        : "s"(m0v), "v"(voff), "s"(sbase)
+        : "memory", "m0");
+}
+
 // Workgroup barrier for the tile loop: LDS accesses of this wave complete,
 // then s_barrier.  Unlike __syncthreads() it does not drain vector memory, so
 // the LDS-DMA gathers of later tiles stay in flight across it.
@@ -318,8 +337,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     __shared__ __attribute__((aligned(1024))) unsigned char s_ring[L::RING_BYTES];
     __shared__ int32_t s_rows_arr[MAX_CHUNK];
     // P exchange: [u][source wave][hi][head lane] x 16 bytes (8 P values), so
-    // a B-operand fragment of the PV MFMA is one contiguous 16-byte read
-    __shared__ __attribute__((aligned(16))) unsigned char s_p[2 * NWAVE * 64 * 16];
+    // a B-operand fragment of the PV MFMA is one contiguous 16-byte read.
+    // bf16 caches keep two (the P of tile it+1 is written while tile it's is read).
+    constexpr int PXB = 2 * NWAVE * 64 * 16;
+    __shared__ __attribute__((aligned(16))) unsigned char s_p[(FP8 ? 1 : 2) * PXB];
     __shared__ int s_misc_arr[16];            // [0..3] wave sums, [4] restart flag
     const lds_ptr T0 = (lds_ptr)s_tile0;
     const lds_ptr T1 = (lds_ptr)s_tile1;
@@ -495,15 +516,15 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             const lds_ptr tb = slot_buf(slot);
             if (i < 8) {
                 const int r = 8 * wave + i;
-                const unsigned char* src;
+                // wave-uniform row: the row address is scalar, the lane part a 32-bit offset
+                const unsigned char* base;
                 if constexpr (L::D512) {
-                    const int32_t id = g.r[i];   // wave-uniform: the pool choice is scalar
-                    const unsigned char* base = (id & POOL2) ? p.kv2 : p.kv;
-                    src = base + (int64_t)(id & (POOL2 - 1)) * p.row_bytes + 16 * (ln ^ nope_sw(r));
+                    const int32_t id = g.r[i];
+                    base = ((id & POOL2) ? p.kv2 : p.kv) + (int64_t)(id & (POOL2 - 1)) * p.row_bytes;
                 } else {
-                    src = p.kv + (int64_t)g.r[i] * BF16_ROW + 16 * (ln ^ nope_sw(r));
+                    base = p.kv + (int64_t)g.r[i] * BF16_ROW;
                 }
-                lds_dma16(src, tb + r * NOPE_STRIDE);
+                lds_dma16_s(base, 16u * (unsigned)(ln ^ nope_sw(r)), tb + r * NOPE_STRIDE);
             } else if constexpr (!L::D512) {
                 const int r = 8 * wave + (ln >> 3);
                 const unsigned char* src =
@@ -701,10 +722,38 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         return pb;
     };
 
-    // ---- one tile: QK^T (+ gathers of a later tile), softmax, PV (+ dequant of the next tile) ----
-    // kt: buffer holding tile `it`; nxt: fp8 only, buffer receiving tile it+1.
-    bool first_tile = true;
-    auto step = [&](int it, lds_cptr kt, lds_ptr nxt) {
+    // Padding rows of a list's last tile get no weight.  Lane (hi, r32), reg r
+    // holds row 8*(r/4) + 4*hi + r%4.  Only the last tile takes the branch; the
+    // empty asm keeps the compiler from turning it into selects (and hoisted
+    // row numbers) that every tile would pay for.
+    auto mask_rows = [&](f32x16& s, int rows_left) {
+        if (rows_left < TILE) {
+            asm volatile("");
+            const int h4 = 4 * opaque(hi);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = 8 * (r >> 2) + h4 + (r & 3);
+                s[r] = row < rows_left ? s[r] : -INFINITY;
+            }
+        }
+    };
+    // the largest score of a list's first tile (rows below rows_left)
+    auto first_max = [&](const f32x16& s, int rows_left) -> float {
+        asm volatile("");
+        const int h4 = 4 * opaque(hi);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = 8 * (r >> 2) + h4 + (r & 3);
+            mx = fmaxf(mx, row < rows_left ? s[r] : -INFINITY);
+        }
+        return fmaxf(mx, __shfl_xor(mx, 32, 64));
+    };
+
+    // ---- S^T = K Q^T of the tile in buffer kt (32 rows x this wave's 32 heads) ----
+    // Software pipeline pinned with scheduling barriers: the K fragment of
+    // k-step ks+KPF is read while MFMA ks runs.
+    auto qk = [&](lds_cptr kt) -> f32x16 {
         // per-lane offsets inside the tile buffer (recomputed per tile)
         const int ln = opaque(lane);
         const int lhi = ln >> 5, lr = ln & 31;
@@ -713,16 +762,34 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         const lds_cptr k_odd = kt + lr * NOPE_STRIDE + 16 * ((2 + lhi) ^ nope_sw(lr));
         const lds_cptr k_rope = kt + ROPE_OFF + 128 * lr;
         const int rsw = rope_sw(lr);
-
-        // ---- S^T = K Q^T (32 rows x 32 heads) ----
-        // Software pipeline pinned with scheduling barriers: the K fragment of
-        // k-step ks+KPF is read while MFMA ks runs; the gathers of tile
-        // it+NPRE are issued between the MFMAs (one load every 4 k-steps).
         constexpr int KPF = L::MX ? 3 : (FP8 ? 4 : 6);   // register-bound for the fp8 formats
         auto k_addr = [&](int ks) -> lds_cptr {
             return ks < KS_NOPE ? ((ks & 1) ? k_odd : k_even) + 64 * (ks >> 1)
                                 : k_rope + 16 * ((2 * (ks - KS_NOPE) + lhi) ^ rsw);
         };
+        u32x4 kb[KPF];
+#pragma unroll
+        for (int i = 0; i < KPF; ++i) kb[i] = lds_ld<u32x4>(k_addr(i));
+        // one accumulator chain: back-to-back dependent MFMAs issue at the full
+        // rate, and two chains would cost 16 adds per tile to combine
+        f32x16 acc = {};
+#pragma unroll
+        for (int ks = 0; ks < L::KS; ++ks) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (L::F16 && ks < KS_NOPE) acc = mfma_f16(kb[ks % KPF], qf[ks], acc);
+            else acc = mfma_bf16(kb[ks % KPF], qf[ks], acc);
+            if (ks + KPF < L::KS) kb[ks % KPF] = lds_ld<u32x4>(k_addr(ks + KPF));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        return acc;
+    };
+
+    // ---- fp8 caches, one tile: QK^T (after the gathers of a later tile), softmax, PV (+ dequant of the next tile) ----
+    // kt: buffer holding tile `it`; nxt: buffer receiving tile it+1.
+    bool first_tile = true;
+    auto step = [&](int it, lds_cptr kt, lds_ptr nxt) {
+        const int ln = opaque(lane);
+        const int lhi = ln >> 5;
         const bool do_issue = it + NPRE < ntiles;
         const int issue_slot = FP8 ? it % 3 : (it + 2) % 3;
         const GatherRows gcur = gnext;
@@ -732,22 +799,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         // while LDS reads are in flight holds the wave far longer.
         if (do_issue) issue_rows(gcur, issue_slot);
         __builtin_amdgcn_sched_barrier(0);
-        u32x4 kb[KPF];
-#pragma unroll
-        for (int i = 0; i < KPF; ++i) kb[i] = lds_ld<u32x4>(k_addr(i));
-        // two accumulator chains (even / odd k-steps): a dependent MFMA chain
-        // issues at about 60 % of the MFMA rate, two interleaved chains at full rate
-        f32x16 sacc2[2] = {f32x16{}, f32x16{}};
-#pragma unroll
-        for (int ks = 0; ks < L::KS; ++ks) {
-            __builtin_amdgcn_sched_barrier(0);
-            f32x16& acc = sacc2[ks & 1];
-            if (L::F16 && ks < KS_NOPE) acc = mfma_f16(kb[ks % KPF], qf[ks], acc);
-            else acc = mfma_bf16(kb[ks % KPF], qf[ks], acc);
-            if (ks + KPF < L::KS) kb[ks % KPF] = lds_ld<u32x4>(k_addr(ks + KPF));
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        f32x16 sacc = sacc2[0] + sacc2[1];
+        f32x16 sacc = qk(kt);
         // row ids of the tile issued in the next step
         if (it + NPRE + 1 < ntiles) gnext = load_rows(it + NPRE + 1);
 
@@ -756,24 +808,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         // regs 0..7 are rows 0..15 (PV k-step u = 0), regs 8..15 rows 16..31.
         const int rows_left = n_valid - it * TILE;
         if (first_tile) {
-            float mx = -INFINITY;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = 8 * (r >> 2) + 4 * hi + (r & 3);
-                mx = fmaxf(mx, row < rows_left ? sacc[r] : -INFINITY);
-            }
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            m_ref = mx * c_s;
+            m_ref = first_max(sacc, rows_left) * c_s;
             first_tile = false;
         }
-        if (rows_left < TILE) {
-            // last tile: the padding rows get no weight
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = 8 * (r >> 2) + 4 * hi + (r & 3);
-                sacc[r] = row < rows_left ? sacc[r] : -INFINITY;
-            }
-        }
+        mask_rows(sacc, rows_left);
         if (ntiles == 1 && it == 0) {
             // Single-tile list: fold the exact sum into the reference, so
             // that p = exp2(s - m_ref) is already normalised when it is
@@ -869,6 +907,94 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         __builtin_amdgcn_sched_barrier(0);
     };
 
+    // ---- bf16 caches: a software-pipelined tile loop ----
+    // Iteration it computes QK^T of tile it+1, then PV of tile it with the
+    // softmax numerators of tile it+1 worked out between its MFMAs, and stores
+    // tile it+1's P into the other P buffer; the next iteration's barrier
+    // publishes it, so a tile costs one workgroup barrier.  The arithmetic and
+    // its order per tile are those of `step` (QK^T, p = exp2(s c - m_ref), the
+    // sums per half, the O accumulation order): both loops give the same bits.
+    // Padding rows of the last tile, and the raw maximum of the pass.
+    auto mask_track = [&](f32x16& s, int j) {
+        mask_rows(s, n_valid - j * TILE);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            float sm = -INFINITY;
+#pragma unroll
+            for (int r = 8 * u; r < 8 * u + 8; ++r) sm = fmaxf(sm, s[r]);
+            s_max = fmaxf(s_max, sm);
+        }
+    };
+    // P of a tile from its numerators, half u (rows 16u..16u+15) into P buffer px;
+    // half 0 before half 1, so the sums accumulate in the same order as in `step`
+    auto p_half = [&](const float* e, int u, lds_ptr px) {
+        const int ln = opaque(lane);
+        float lt = 0.0f;
+#pragma unroll
+        for (int r = 8 * u; r < 8 * u + 8; ++r) lt += e[r];
+        l_lane += lt;
+        lds_st<u32x4>(px + ((u * NWAVE + wave) * 64 + ln) * 16, to_p(e + 8 * u));
+    };
+    // tile 0 of a pass: the reference (first pass), padding, the one-tile fold, P
+    auto soft_first = [&](f32x16& s, lds_ptr px) {
+        if (first_tile) {
+            m_ref = first_max(s, n_valid) * c_s;
+            first_tile = false;
+        }
+        mask_track(s, 0);
+        if (ntiles == 1) {
+            float lt = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) lt += __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c_s, -m_ref));
+            lt += __shfl_xor(lt, 32, 64);
+            if constexpr (L::D512)
+                if (p.attn_sink) lt += __builtin_amdgcn_exp2f(__builtin_fmaf(p.attn_sink[head], LOG2E, -m_ref));
+            m_ref += __builtin_amdgcn_logf(lt);
+        }
+        float e[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) e[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c_s, -m_ref));
+        p_half(e, 0, px);
+        p_half(e, 1, px);
+    };
+    // O^T += V^T P^T for the tile in kv_t with P from px_cur; with_exp
+    // (std::true_type): the numerators of the next tile's scores sn go to en,
+    // two per MFMA group (group (u, m) gives en[8u + 2m], en[8u + 2m + 1])
+    auto pv_pipe = [&](lds_cptr kv_t, lds_cptr px_cur, const f32x16& sn, float* en, auto with_exp) {
+        const int ln = opaque(lane);
+        const int lhi = ln >> 5;
+        const int g16 = ln >> 4, i16 = ln & 15, rr = i16 >> 2, pp = i16 & 3;
+        const int vx = 2 * (g16 & 1) + (pp >> 1);
+        const lds_cptr v_a = kv_t + (4 * lhi + rr) * NOPE_STRIDE + 16 * (vx ^ lhi) + 8 * (pp & 1) + 256 * wave;
+        const lds_cptr v_b = kv_t + (4 * lhi + rr + 8) * NOPE_STRIDE + 16 * (vx ^ (lhi + 2)) + 8 * (pp & 1) + 256 * wave;
+        auto v_frag = [&](int u, int m) -> u32x4 {
+            const s16x4 va = lds_read_tr16(v_a + 16 * u * NOPE_STRIDE + 64 * m);
+            const s16x4 vb = lds_read_tr16(v_b + 16 * u * NOPE_STRIDE + 64 * m);
+            return __builtin_bit_cast(u32x4, __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7));
+        };
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            u32x4 pbf[NWAVE];
+#pragma unroll
+            for (int h = 0; h < NWAVE; ++h) pbf[h] = lds_ld<u32x4>(px_cur + ((u * NWAVE + h) * 64 + ln) * 16);
+            u32x4 va_cur = v_frag(u, 0);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                __builtin_amdgcn_sched_barrier(0);
+                const u32x4 va_nxt = m + 1 < 4 ? v_frag(u, m + 1) : va_cur;
+#pragma unroll
+                for (int h = 0; h < NWAVE; ++h) mfma_o<L::F16>(o[4 * m + h], va_cur, pbf[h]);
+                if constexpr (decltype(with_exp)::value) {
+                    const int r0 = 8 * u + 2 * m;
+                    en[r0] = __builtin_amdgcn_exp2f(__builtin_fmaf(sn[r0], c_s, -m_ref));
+                    en[r0 + 1] = __builtin_amdgcn_exp2f(__builtin_fmaf(sn[r0 + 1], c_s, -m_ref));
+                }
+                va_cur = va_nxt;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
     for (int pass = 0;; ++pass) {
 #pragma unroll
         for (int mb = 0; mb < D_VO / 32; ++mb) o[mb] = f32x16{};
@@ -904,12 +1030,40 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                 }
             }
         } else {
-            int slot_cur = 0;        // ring slot of tile `it`
-            for (int it = 0; it < ntiles; ++it) {
-                wait_tiles(it + 1 < ntiles ? 1 : 0);
+            // ring slot of tile j: j % 3.  Tiles 0 and 1 were issued above.
+            if (ntiles > 0) {
+                wait_tiles(ntiles > 1 ? 1 : 0);    // tile 0 landed
                 tile_barrier();
-                step(it, slot_buf(slot_cur), nullptr);
-                slot_cur = slot_cur == 2 ? 0 : slot_cur + 1;
+                f32x16 s0 = qk(slot_buf(0));
+                soft_first(s0, PX);
+            }
+            int slot_cur = 0;        // ring slot of tile `it`
+            // every tile but the last: QK^T of the next tile, PV of this one
+            for (int it = 0; it + 1 < ntiles; ++it) {
+                const int slot_nxt = slot_cur == 2 ? 0 : slot_cur + 1;
+                // tile it+1 landed (the only tile in flight); after the barrier
+                // every wave's P of tile it is visible and every wave is done
+                // with iteration it-1, whose ring slot receives tile it+2
+                wait_vm<0>();
+                tile_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                if (it + NPRE < ntiles) issue_rows(gnext, slot_nxt == 2 ? 0 : slot_nxt + 1);
+                __builtin_amdgcn_sched_barrier(0);
+                f32x16 sn = qk(slot_buf(slot_nxt));
+                if (it + NPRE + 1 < ntiles) gnext = load_rows(it + NPRE + 1);
+                mask_track(sn, it + 1);
+                float en[16];
+                pv_pipe(slot_buf(slot_cur), PX + (it & 1) * PXB, sn, en, std::true_type{});
+                const lds_ptr px_nxt = PX + ((it + 1) & 1) * PXB;
+                p_half(en, 0, px_nxt);
+                p_half(en, 1, px_nxt);
+                slot_cur = slot_nxt;
+            }
+            if (ntiles > 0) {
+                // the last tile: PV only (its P is published by this barrier)
+                tile_barrier();
+                float en[16];
+                pv_pipe(slot_buf(slot_cur), PX + ((ntiles - 1) & 1) * PXB, f32x16{}, en, std::false_type{});
             }
         }
         // drain in-flight gathers before the ring can be reused or left
