@@ -485,6 +485,21 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         int32_t rope;                             // bf16: row of this lane's RoPE chunk
     };
     const int my_loads = FP8 ? (wave < L::LOADS - NWAVE * (FP8_LPW - 1) ? FP8_LPW : FP8_LPW - 1) : L::LPW;
+    // 656-B rows: lane chunk c16 = 64 k + lane of load k = wave + 4 i lies in
+    // row rt = c16 / 41 of the tile, at chunk c = c16 - 41 rt.  Both are fixed
+    // per lane and load, so they are computed once and packed in one register:
+    // bits 0..15 the byte offset of the row's id in the row list (rt clamped
+    // to 31: the last load's spare lanes read chunks c < 32 of row 31 into the
+    // slot padding), bits 16..31 the chunk's byte offset in the row.
+    uint32_t f_rc[FP8_LPW] = {};
+    if constexpr (L::F16) {
+#pragma unroll
+        for (int i = 0; i < FP8_LPW; ++i) {
+            const unsigned c16 = 64 * (wave + NWAVE * i) + lane;
+            const unsigned rt = c16 / 41u;
+            f_rc[i] = 4u * (rt < TILE - 1 ? rt : TILE - 1) | (16u * (c16 - 41u * rt)) << 16;
+        }
+    }
     auto load_rows = [&](int ti) -> GatherRows {
         const LDS_AS int32_t* rows = s_rows + ti * TILE;
         const int ln = opaque(lane);
@@ -500,9 +515,8 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                     const int k = wave + NWAVE * i;                      // load of the tile (uniform)
                     g.r[i] = rows[k < 16 ? 2 * k + (ln >> 5) : (k < 20 ? 8 * (k - 16) + (ln >> 3) : (ln & 31))];
                 } else {
-                    const unsigned c16 = 64 * (wave + NWAVE * i) + ln;   // linear chunk of the raw tile
-                    const unsigned rt = __umul24(c16, 1599u) >> 16;     // c16 / 41
-                    g.r[i] = rows[rt < TILE - 1 ? rt : TILE - 1];
+                    // (an opaque copy: the unpacked halves would be hoisted out of the loop)
+                    g.r[i] = lds_ld<int32_t>((lds_cptr)rows + ((unsigned)opaque((int)f_rc[i]) & 0xFFFFu));
                 }
             }
             g.rope = 0;
@@ -564,10 +578,8 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                                : (k < 20 ? p.kv_ro + row * p.kvr_st + 16 * (ln & 7) : p.kv_sc + row * p.kvs_st);
                     lds_dma16(src, RING + slot * RAW_STRIDE + 1024 * k);
                 } else {
-                    const unsigned c16 = 64 * k + ln;
-                    const unsigned c = c16 - 41u * (__umul24(c16, 1599u) >> 16);
-                    const uint64_t ch = row * 41u + c;   // 16-byte chunk of the cache
-                    lds_dma16(p.kv + (ch << 4), RING + slot * RAW_STRIDE + 1024 * k);
+                    lds_dma16(p.kv + (row * FP8_ROW + ((unsigned)opaque((int)f_rc[i]) >> 16)),
+                              RING + slot * RAW_STRIDE + 1024 * k);
                 }
             }
         }
@@ -754,8 +766,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // Software pipeline pinned with scheduling barriers: the K fragment of
     // k-step ks+KPF is read while MFMA ks runs.
     auto qk = [&](lds_cptr kt) -> f32x16 {
-        // per-lane offsets inside the tile buffer (recomputed per tile)
-        const int ln = opaque(lane);
+        const int ln = lane;
         const int lhi = ln >> 5, lr = ln & 31;
         // K fragment of k-step ks (A operand of S^T = K Q^T): row lr, chunk 2ks+hi
         const lds_cptr k_even = kt + lr * NOPE_STRIDE + 16 * (lhi ^ nope_sw(lr));
@@ -961,7 +972,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // (std::true_type): the numerators of the next tile's scores sn go to en,
     // two per MFMA group (group (u, m) gives en[8u + 2m], en[8u + 2m + 1])
     auto pv_pipe = [&](lds_cptr kv_t, lds_cptr px_cur, const f32x16& sn, float* en, auto with_exp) {
-        const int ln = opaque(lane);
+        const int ln = lane;
         const int lhi = ln >> 5;
         const int g16 = ln >> 4, i16 = ln & 15, rr = i16 >> 2, pp = i16 & 3;
         const int vx = 2 * (g16 & 1) + (pp >> 1);
