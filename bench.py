@@ -45,8 +45,10 @@ CONFIGS = {
                causal=False),
     "c2": dict(kind="decode", B=64, s_q=1, seq=32768, block=64, topk=2048, pad=0, fp8=False,
                causal=False),
+    # three (Q, top-k) sets alternate step by step: one set's 417 MB could partly stay in
+    # the 256 MB MALL between steps
     "c3": dict(kind="decode", B=128, s_q=2, seq=65536, block=64, topk=2048, pad=0, fp8=True,
-               causal=True),
+               causal=True, sets=3),
     "c4": dict(kind="decode", B=4, s_q=1, seq=None, block=64, topk=2048, pad=0, fp8=False,
                causal=False, splits=8),
     "c5": dict(kind="prefill", N=8192, topk=2048),
@@ -61,7 +63,8 @@ CONFIGS = {
 NAMES = {
     "c1": "bf16 sparse MLA decode B=2 H=128 top-k 2048 (256 pad) flat KV 8192",
     "c2": "bf16 sparse MLA decode B=64 H=128 top-k 2048 paged(64) seq 32768",
-    "c3": "fp8-KV(656B) sparse MLA decode B=128 s_q=2 (MTP) H=128 top-k 2048 paged(64) seq 65536 causal",
+    "c3": "fp8-KV(656B) sparse MLA decode B=128 s_q=2 (MTP) H=128 top-k 2048 paged(64) seq 65536 causal"
+          " (3 Q / top-k sets alternate step by step)",
     "c4": "bf16 split-top-k decode B=4 H=128 top-k<=2048 seq U[1024,131072] 8 splits + combine",
     "c5": "bf16 sparse MLA prefill N=8192 H=128 top-k 2048 from [0,t]",
     "mx": ("MXFP8 split-stream sparse MLA decode (E8M0 per 32, CSR) B=128 s_q=2 (MTP) H=128, "
@@ -110,17 +113,25 @@ def make_decode(cfg, dev, seed=2026):
     else:
         kv = torch.randn((rows, D_QK), generator=g, device=dev).to(torch.bfloat16)
     # distinct top-k positions per query token (scattered order), causal bound, -1 padding
-    idx = torch.full((B, s_q, topk), -1, dtype=torch.int32, device=dev)
-    for b in range(B):
-        L = int(seq_lens[b])
-        for t in range(s_q):
-            hi = L - s_q + t + 1 if cfg["causal"] else L
-            n = min(topk - cfg["pad"], hi)
-            r = torch.rand((hi,), generator=g, device=dev)
-            idx[b, t, :n] = torch.topk(r, n).indices.to(torch.int32)
+    def top_k_set():
+        idx = torch.full((B, s_q, topk), -1, dtype=torch.int32, device=dev)
+        for b in range(B):
+            L = int(seq_lens[b])
+            for t in range(s_q):
+                hi = L - s_q + t + 1 if cfg["causal"] else L
+                n = min(topk - cfg["pad"], hi)
+                r = torch.rand((hi,), generator=g, device=dev)
+                idx[b, t, :n] = torch.topk(r, n).indices.to(torch.int32)
+        return idx
+    idx = top_k_set()
+    # further (Q, top-k) sets for the rotated timing loop; set 0 is (q, idx)
+    sets = [(q, idx)]
+    for _ in range(cfg.get("sets", 1) - 1):
+        q_k = torch.randn((B, s_q, H, D_QK), generator=g, device=dev).to(torch.bfloat16)
+        sets.append((q_k, top_k_set()))
     torch.cuda.synchronize()
     return dict(q=q, kv=kv, idx=idx, seq_lens=seq_lens, block_table=block_table, block_size=bs or 1,
-                kv_batch_stride=0 if bs else max_len, causal=cfg["causal"])
+                kv_batch_stride=0 if bs else max_len, causal=cfg["causal"], sets=sets)
 
 
 def decode_call(d, splits=0, out=None, lse=None, ws=None):
@@ -407,16 +418,20 @@ def count_valid(d) -> int:
 
 def prepared_decode(a, ws):
     """One decode step as a direct C-ABI call with arguments built once: the timed loop
-    measures the library, not Python argument checking."""
+    measures the library, not Python argument checking.  `a` may be a list of argument
+    blocks (rotated input sets), used in turn."""
     import ctypes
     import torch
     from opfoundry_amd.abi import check, load_library
     fn = load_library().dsa_mla_decode
-    ap, wp, wb = ctypes.byref(a), ws.data_ptr(), ws.numel()
+    aps = [ctypes.byref(x) for x in (a if isinstance(a, list) else [a])]
+    wp, wb = ws.data_ptr(), ws.numel()
     st = torch.cuda.current_stream().cuda_stream
+    turn = [0]
 
     def step():
-        rc = fn(ap, wp, wb, st)
+        rc = fn(aps[turn[0]], wp, wb, st)
+        turn[0] = (turn[0] + 1) % len(aps)
         if rc:
             check(rc, "dsa_mla_decode")
     return step
@@ -648,14 +663,15 @@ def main():
     splits = cfg.get("splits", 0)
     out, lse = decode_call(d, splits)
     from opfoundry_amd import dsa
-    a = dsa.make_decode_args(d["q"], d["kv"], d["idx"], SM_SCALE, out, lse, seq_lens=d["seq_lens"],
-                             block_table=d["block_table"], block_size=d["block_size"],
-                             causal=d["causal"], num_splits=splits,
-                             kv_batch_stride=d["kv_batch_stride"])
+    a_sets = [dsa.make_decode_args(q_k, d["kv"], idx_k, SM_SCALE, out, lse, seq_lens=d["seq_lens"],
+                                   block_table=d["block_table"], block_size=d["block_size"],
+                                   causal=d["causal"], num_splits=splits,
+                                   kv_batch_stride=d["kv_batch_stride"]) for q_k, idx_k in d["sets"]]
+    a = a_sets[0]
     ns = dsa.decode_num_splits(a)
     ws_bytes = dsa.decode_workspace_size(a)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    step = prepared_decode(a, ws)
+    step = prepared_decode(a_sets, ws)
 
     log(f"timing {args.steps} steps after warm-up (splits={ns})")
     n_warm = warm_up(step, args.warmup)
