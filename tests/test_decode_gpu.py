@@ -92,6 +92,34 @@ def test_small_topk(dev, topk):
     check(c, dev, f"topk={topk}")
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+def test_reference_restart(dev, fp8):
+    """The kernel's softmax keeps the first tile's maximum as a fixed reference; a later score
+    more than 100 (bf16) / 15 (fp16 path) above it in log2 units makes the workgroup rerun its
+    tiles against the exact maximum.  Token 0 gets an all-ones Q and two spike rows, in tiles 1
+    and 2: 7.0 in dims 0..255 (score 1792) and in dims 256..510 (score 1785), about 200 log2
+    units above the rest.  7.0 = 448 * 2^-6 is exact in bf16, fp16 and the fp8 row (scale
+    amax / 448 = 2^-6), so the result is a plain 1 : e^-0.505 mixture of the two V halves."""
+    c = paged_case(seed=41, B=2, seq_len=2048, topk=200, fp8=fp8)   # 7 tiles per token
+    q = oracle.bf16_to_f32(c.q)
+    q[0, 0] = 1.0
+    c.q = oracle.bf16_bits(q)
+
+    def row_of(j):
+        return int(c.block_table[0][j // c.block_size]) * c.block_size + j % c.block_size
+
+    ra, rb = row_of(int(c.indices[0, 0, 40])), row_of(int(c.indices[0, 0, 75]))
+    spike = np.zeros((2, D_QK), np.float32)
+    spike[0, :256] = 7.0
+    spike[1, 256:511] = 7.0
+    c.kv[[ra, rb]] = oracle.quantize_rows_656(spike) if fp8 else oracle.bf16_bits(spike)
+    o, l, o_ref, l_ref = check(c, dev, f"reference restart fp8={fp8}")
+    # the case does exercise the mixture: both V halves carry weight in token 0's output
+    w = 7.0 * np.exp(-7 * SM_SCALE) / (1 + np.exp(-7 * SM_SCALE))
+    of = oracle.bf16_to_f32(o).reshape(-1, 128, 512)[0]
+    assert np.allclose(of[:, :256], 7.0 - w, atol=2e-2) and np.allclose(of[:, 256:511], w, atol=2e-2)
+
+
 def test_all_invalid(dev):
     """No valid entry: O = 0 and LSE = +inf (host.cc:486-489)."""
     c = paged_case(seed=16, B=2, seq_len=512, topk=64)
