@@ -838,10 +838,9 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                 if (p.attn_sink) lt += __builtin_amdgcn_exp2f(__builtin_fmaf(p.attn_sink[head], LOG2E, -m_ref));
             m_ref += __builtin_amdgcn_logf(lt);
         }
-        // P in two halves: with the reference fixed, p of a row depends on its
-        // own score only, so regs 0..7 (rows 0..15, the PV k-step u = 0) are
-        // exchanged first and the exponentials of regs 8..15 run between the
-        // MFMAs of PV u = 0.
+        // P of both halves, then one barrier: the wave's VALU work does not
+        // overlap its own MFMAs, so exponentials placed between the PV MFMAs
+        // would save nothing and a second barrier would cost one.
         float e[16];
         auto p_exp = [&](int r) { e[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], c_s, -m_ref)); };
         auto p_store = [&](int u) {
@@ -856,9 +855,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             lds_st<u32x4>(PX + ((u * NWAVE + wave) * 64 + ln) * 16, to_p(e + 8 * u));
         };
 #pragma unroll
-        for (int r = 0; r < 8; ++r) p_exp(r);
+        for (int r = 0; r < 16; ++r) p_exp(r);
         p_store(0);
-        tile_barrier();     // every wave's P of rows 0..15 is visible
+        p_store(1);
+        tile_barrier();     // every wave's P is visible
 
         // ---- O^T[128 dims of this wave x 128 heads] += V^T P^T ----
         // Transposed V reads: 16-lane group g16 reads rows R..R+3 (lane
@@ -879,10 +879,6 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             int step_i = 0;   // MFMA-group counter (8 groups of 4 MFMAs)
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                if (u == 1) {
-                    p_store(1);
-                    tile_barrier();     // every wave's P of rows 16..31 is visible
-                }
                 u32x4 pbf[NWAVE];
 #pragma unroll
                 for (int h = 0; h < NWAVE; ++h) pbf[h] = lds_ld<u32x4>(PX + ((u * NWAVE + h) * 64 + ln) * 16);
@@ -893,10 +889,6 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                     const u32x4 va_nxt = m + 1 < 4 ? v_frag(u, m + 1) : va_cur;
 #pragma unroll
                     for (int h = 0; h < NWAVE; ++h) mfma_o<L::F16>(o[4 * m + h], va_cur, pbf[h]);
-                    if (u == 0) {
-                        p_exp(8 + 2 * m);
-                        p_exp(9 + 2 * m);
-                    }
                     if constexpr (FP8) {
                         // piece j: loads in MFMA group j, conversion + store in group j+1
                         const int j = step_i;
