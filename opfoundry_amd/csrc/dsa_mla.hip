@@ -765,7 +765,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // ---- S^T = K Q^T of the tile in buffer kt (32 rows x this wave's 32 heads) ----
     // Software pipeline pinned with scheduling barriers: the K fragment of
     // k-step ks+KPF is read while MFMA ks runs.
-    auto qk = [&](lds_cptr kt) -> f32x16 {
+    auto qk = [&](lds_cptr kt, auto&& per_step) -> f32x16 {
         const int ln = lane;
         const int lhi = ln >> 5, lr = ln & 31;
         // K fragment of k-step ks (A operand of S^T = K Q^T): row lr, chunk 2ks+hi
@@ -790,6 +790,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             if (L::F16 && ks < KS_NOPE) acc = mfma_f16(kb[ks % KPF], qf[ks], acc);
             else acc = mfma_bf16(kb[ks % KPF], qf[ks], acc);
             if (ks + KPF < L::KS) kb[ks % KPF] = lds_ld<u32x4>(k_addr(ks + KPF));
+            per_step(ks);
         }
         __builtin_amdgcn_sched_barrier(0);
         return acc;
@@ -810,7 +811,20 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         // while LDS reads are in flight holds the wave far longer.
         if (do_issue) issue_rows(gcur, issue_slot);
         __builtin_amdgcn_sched_barrier(0);
-        f32x16 sacc = qk(kt);
+        // V4 fp8 rows: the next tile's dequant runs between the QK^T MFMAs
+        // (piece j loads at k-step 4j, is converted and stored at 4j + 2):
+        // measured 2 % faster there, neutral for the other fp8 formats, which
+        // keep it between the PV MFMAs
+        constexpr bool DEQ_QK = L::V4MX;
+        DeqPiece dq[2];
+        const lds_cptr draw = FP8 ? RING + ((it + 1) % 3) * RAW_STRIDE : kt;
+        constexpr int NPIECE = L::D512 ? DEQ_PIECES - 1 : DEQ_PIECES;
+        f32x16 sacc = qk(kt, [&](int ks) {
+            if constexpr (DEQ_QK) {
+                if ((ks & 3) == 0 && ks / 4 < NPIECE) dq[(ks / 4) & 1] = deq_load(draw, ks / 4);
+                if ((ks & 3) == 2 && ks / 4 < NPIECE) deq_store(nxt, ks / 4, dq[(ks / 4) & 1]);
+            }
+        });
         // row ids of the tile issued in the next step
         if (it + NPRE + 1 < ntiles) gnext = load_rows(it + NPRE + 1);
 
@@ -869,13 +883,11 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             const int vx = 2 * (g16 & 1) + (pp >> 1);
             const lds_cptr v_a = kt + (4 * lhi + rr) * NOPE_STRIDE + 16 * (vx ^ lhi) + 8 * (pp & 1) + 256 * wave;
             const lds_cptr v_b = kt + (4 * lhi + rr + 8) * NOPE_STRIDE + 16 * (vx ^ (lhi + 2)) + 8 * (pp & 1) + 256 * wave;
-            const lds_cptr draw = FP8 ? RING + ((it + 1) % 3) * RAW_STRIDE : kt;
             auto v_frag = [&](int u, int m) -> u32x4 {
                 const s16x4 va = lds_read_tr16(v_a + 16 * u * NOPE_STRIDE + 64 * m);
                 const s16x4 vb = lds_read_tr16(v_b + 16 * u * NOPE_STRIDE + 64 * m);
                 return __builtin_bit_cast(u32x4, __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7));
             };
-            DeqPiece dq[2];
             int step_i = 0;   // MFMA-group counter (8 groups of 4 MFMAs)
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
@@ -889,7 +901,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                     const u32x4 va_nxt = m + 1 < 4 ? v_frag(u, m + 1) : va_cur;
 #pragma unroll
                     for (int h = 0; h < NWAVE; ++h) mfma_o<L::F16>(o[4 * m + h], va_cur, pbf[h]);
-                    if constexpr (FP8) {
+                    if constexpr (FP8 && !DEQ_QK) {
                         // piece j: loads in MFMA group j, conversion + store in group j+1
                         const int j = step_i;
                         dq[j & 1] = deq_load(draw, j);
@@ -899,7 +911,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                     ++step_i;
                 }
             }
-            if constexpr (FP8) {
+            if constexpr (FP8 && !DEQ_QK) {
                 // pieces 0..7 were loaded in the 8 MFMA groups, 0..6 stored
                 static_assert(DEQ_PIECES == 9, "dequant pieces vs MFMA groups");
                 __builtin_amdgcn_sched_barrier(0);
@@ -1037,7 +1049,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             if (ntiles > 0) {
                 wait_tiles(ntiles > 1 ? 1 : 0);    // tile 0 landed
                 tile_barrier();
-                f32x16 s0 = qk(slot_buf(0));
+                f32x16 s0 = qk(slot_buf(0), [](int) {});
                 soft_first(s0, PX);
             }
             int slot_cur = 0;        // ring slot of tile `it`
@@ -1052,7 +1064,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                 __builtin_amdgcn_sched_barrier(0);
                 if (it + NPRE < ntiles) issue_rows(gnext, slot_nxt == 2 ? 0 : slot_nxt + 1);
                 __builtin_amdgcn_sched_barrier(0);
-                f32x16 sn = qk(slot_buf(slot_nxt));
+                f32x16 sn = qk(slot_buf(slot_nxt), [](int) {});
                 if (it + NPRE + 1 < ntiles) gnext = load_rows(it + NPRE + 1);
                 mask_track(sn, it + 1);
                 float en[16];
