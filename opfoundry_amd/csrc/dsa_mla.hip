@@ -773,7 +773,8 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         const lds_cptr k_odd = kt + lr * NOPE_STRIDE + 16 * ((2 + lhi) ^ nope_sw(lr));
         const lds_cptr k_rope = kt + ROPE_OFF + 128 * lr;
         const int rsw = rope_sw(lr);
-        constexpr int KPF = L::MX ? 3 : (FP8 ? 4 : 6);   // register-bound for the fp8 formats
+        // K prefetch depth, per format by measurement (deeper spilled or ran slower)
+        constexpr int KPF = L::V4MX ? 4 : (L::MX ? 3 : (FP8 ? 4 : 6));
         auto k_addr = [&](int ks) -> lds_cptr {
             return ks < KS_NOPE ? ((ks & 1) ? k_odd : k_even) + 64 * (ks >> 1)
                                 : k_rope + 16 * ((2 * (ks - KS_NOPE) + lhi) ^ rsw);
