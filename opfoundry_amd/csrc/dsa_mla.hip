@@ -878,7 +878,8 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         // ---- O^T[128 dims of this wave x 128 heads] += V^T P^T ----
         // Transposed V reads: 16-lane group g16 reads rows R..R+3 (lane
         // 4rr+pp: row R+rr, dims d0+4pp..+3) with R = 16u + 4hi and R + 8.
-        // fp8: the dequant of the next tile runs between the MFMAs.
+        // 656-B and MXFP8 rows: the dequant of the next tile runs between
+        // these MFMAs (V4 fp8 rows: between the QK^T MFMAs above).
         {
             const int g16 = ln >> 4, i16 = ln & 15, rr = i16 >> 2, pp = i16 & 3;
             const int vx = 2 * (g16 & 1) + (pp >> 1);
