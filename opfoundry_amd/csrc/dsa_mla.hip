@@ -505,8 +505,14 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         const int ln = opaque(lane);
         GatherRows g;
         if constexpr (!FP8) {
+            // the wave's 8 row ids: two 16-byte reads (32-byte aligned)
+            const u32x4 ra = lds_ld<u32x4>((lds_cptr)(rows + 8 * wave));
+            const u32x4 rb = lds_ld<u32x4>((lds_cptr)(rows + 8 * wave + 4));
 #pragma unroll
-            for (int i = 0; i < TILE / NWAVE; ++i) g.r[i] = __builtin_amdgcn_readfirstlane(rows[8 * wave + i]);
+            for (int i = 0; i < 4; ++i) {
+                g.r[i] = __builtin_amdgcn_readfirstlane((int)ra[i]);
+                g.r[4 + i] = __builtin_amdgcn_readfirstlane((int)rb[i]);
+            }
             g.rope = rows[8 * wave + (ln >> 3)];
         } else {
 #pragma unroll
