@@ -94,3 +94,38 @@ def test_prefill_v4_padded_row_stride(dev):
                                   ts(ide), scale)
     torch.cuda.synchronize()
     assert_parity(bits(out), lse.cpu().numpy(), o_ref, l_ref, "V4 prefill padded stride")
+
+
+def test_prefill_v4_reference_restart(dev):
+    """The fixed-reference softmax's rerun on 512-value rows with a sink: query 8 gets an
+    all-ones Q and two prefix rows (list entries 40 and 75, tiles 1 and 2) holding 8.0 in
+    dims 0..255 (score 2048) and 256..510 (score 2040), about 126 log2 units above the rest.
+    8.0 is exact in bf16, so the output must also be the closed-form mixture
+    1 : e^(-8 scale) of the two V halves (the sink's weight is negligible).
+    The two rows are appended to the pool so that no other query's list names them:
+    a random query against them would give outputs near 8, where one bf16 step is
+    0.03 to 0.06 and the 2e-2 bar no longer applies."""
+    print("[case] V4 prefill reference restart", flush=True)
+    q, ukv, xkv, sink, ipp, idp, ipe, ide = v4_inputs(47)
+    scale = 1.0 / np.sqrt(D)
+    i0 = 8
+    qf = oracle.bf16_to_f32(q)
+    qf[i0] = 1.0
+    q = oracle.bf16_bits(qf)
+    spike = np.zeros((2, D), np.float32)
+    spike[0, :256] = 8.0
+    spike[1, 256:511] = 8.0
+    ra, rb = ukv.shape[0], ukv.shape[0] + 1
+    ukv = np.concatenate([ukv, oracle.bf16_bits(spike)])
+    idp[ipp[i0] + 40], idp[ipp[i0] + 75] = ra, rb
+    o_ref, l_ref = oracle.mla_prefill_v4(q, ukv, xkv, sink, ipp, idp, ipe, ide, scale)
+    ts = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    out, lse = dsa.mla_prefill_v4(t16(q, dev), t16(ukv, dev), t16(xkv, dev), ts(sink), ts(ipp), ts(idp),
+                                  ts(ipe), ts(ide), scale)
+    torch.cuda.synchronize()
+    o = bits(out)
+    e = assert_parity(o, lse.cpu().numpy(), o_ref, l_ref, "V4 prefill reference restart")
+    print(f"[case] max|dO|={e[0]:.3e} max rel dLSE={e[1]:.3e}", flush=True)
+    w = 8.0 * np.exp(-8 * scale) / (1 + np.exp(-8 * scale))
+    oi = oracle.bf16_to_f32(o)[i0]
+    assert np.allclose(oi[:, :256], 8.0 - w, atol=2e-2) and np.allclose(oi[:, 256:511], w, atol=2e-2)

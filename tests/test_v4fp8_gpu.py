@@ -126,3 +126,38 @@ def test_prefill_v4_fp8_padded_streams(dev):
     o1, l1 = run((pad(qd[0], 528), pad(qd[1], 72)), (pad(ud[0], 528), pad(ud[1], 72)),
                  (pad(xd[0], 528), pad(xd[1], 72)), sink, lists, scale, dev)
     assert (o1 == o0).all() and np.array_equal(l1, l0)
+
+
+def test_prefill_v4_fp8_reference_restart(dev):
+    """The rerun of the fixed-reference softmax on V4 fp8 rows: query 8 gets Q = 1 (code 1.0,
+    scale 2^0; RoPE bf16 1.0) and two prefix rows (list entries 40 and 75, tiles 1 and 2)
+    holding 8.0 (code 1.0 under an E8M0 scale of 2^3) in dims 0..255 and in dims 256..447 plus
+    bf16 8.0 in RoPE dims 448..510: scores 2048 and 2040, about 126 log2 units above the
+    rest.  Every value is exact, so the output must also be the closed-form mixture.
+    The two rows are appended to the pool so that no other query's list names them
+    (outputs near 8 would put one bf16 step above the 2e-2 bar)."""
+    print("[case] V4 fp8 prefill reference restart", flush=True)
+    q, ukv, xkv, sink, lists = v4fp8_inputs(67)
+    scale = 1.0 / np.sqrt(512)
+    ipp, idp = lists[0], lists[1]
+    i0 = 8
+    q[0][i0] = 0
+    q[0][i0, :, :448] = 0x38          # e4m3 1.0
+    q[0][i0, :, 448:462] = 127        # E8M0 2^0
+    q[1][i0] = 0x3F80                 # bf16 1.0
+    codes = np.zeros((2,) + ukv[0].shape[1:], ukv[0].dtype)
+    rope = np.zeros((2,) + ukv[1].shape[1:], ukv[1].dtype)
+    codes[:, 448:462] = 130           # E8M0 2^3
+    codes[0, :256] = 0x38             # 8.0 in dims 0..255
+    codes[1, 256:448] = 0x38          # 8.0 in dims 256..447
+    rope[1, :63] = 0x4100             # bf16 8.0 in dims 448..510
+    ra, rb = ukv[0].shape[0], ukv[0].shape[0] + 1
+    ukv = (np.concatenate([ukv[0], codes]), np.concatenate([ukv[1], rope]))
+    idp[ipp[i0] + 40], idp[ipp[i0] + 75] = ra, rb
+    o_ref, l_ref = oracle.mla_prefill_v4_fp8(*q, *ukv, *xkv, sink, *lists, scale)
+    o, l = run(*to_dev(q, ukv, xkv, dev), sink, lists, scale, dev)
+    e = assert_parity(o, l, o_ref, l_ref, "V4 fp8 prefill reference restart")
+    print(f"[case] max|dO|={e[0]:.3e} max rel dLSE={e[1]:.3e}", flush=True)
+    w = 8.0 * np.exp(-8 * scale) / (1 + np.exp(-8 * scale))
+    oi = oracle.bf16_to_f32(o)[i0]
+    assert np.allclose(oi[:, :256], 8.0 - w, atol=2e-2) and np.allclose(oi[:, 256:511], w, atol=2e-2)
