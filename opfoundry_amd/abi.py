@@ -36,7 +36,7 @@ ERRORS = {
     -8: "DSA_ERR_HIP",
 }
 
-# Every symbol include/dsa_mla.h declares, in declaration order.
+# Every symbol include/*.h declares (dsa_mla.h, then dsa_topk.h), in declaration order.
 EXPORTED_SYMBOLS = (
     "dsa_mla_decode_workspace_size",
     "dsa_mla_decode_num_splits",
@@ -51,6 +51,7 @@ EXPORTED_SYMBOLS = (
     "dsa_mla_prefill_v4",
     "dsa_mla_prefill_v4_fp8",
     "dsa_kv_quantize_fp8",
+    "dsa_topk_indices",
     "dsa_mla_strerror",
     "dsa_mla_abi_version",
 )
@@ -191,6 +192,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.dsa_mla_prefill_v4.argtypes = [ctypes.POINTER(PrefillV4Args), _vp]
     lib.dsa_mla_prefill_v4_fp8.argtypes = [ctypes.POINTER(PrefillV4Fp8Args), _vp]
     lib.dsa_kv_quantize_fp8.argtypes = [_vp, _i64, _i64, _vp, _i64, _vp, _vp]
+    lib.dsa_topk_indices.argtypes = [_vp, _i64, _vp, _i32, _i32, _i32, _vp, _i64, _vp]
     lib.dsa_mla_strerror.argtypes = [ctypes.c_int]
     lib.dsa_mla_strerror.restype = ctypes.c_char_p
     lib.dsa_mla_abi_version.argtypes = []

@@ -15,6 +15,7 @@ import sys
 from .abi import LIB_PATH, PKG_DIR
 
 SRC = os.path.join(PKG_DIR, "csrc", "dsa_mla.hip")
+SRCS = [SRC, os.path.join(PKG_DIR, "csrc", "dsa_topk.hip")]
 INCLUDE = os.path.normpath(os.path.join(PKG_DIR, "..", "include"))
 
 # Packed-fp32 VALU ops are disabled for all device code: only ordinary
@@ -41,7 +42,7 @@ def hipcc() -> str:
 def build(verbose: bool = False, extra_flags: list[str] | None = None) -> str:
     os.makedirs(os.path.dirname(LIB_PATH), exist_ok=True)
     tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, *(extra_flags or []), f"-I{INCLUDE}", SRC, "-o", tmp]
+    cmd = [hipcc(), *HIPCC_FLAGS, *(extra_flags or []), f"-I{INCLUDE}", *SRCS, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -402,6 +402,38 @@ def quantize_kv_fp8(src: torch.Tensor, dst: Optional[torch.Tensor] = None,
     return dst
 
 
+def topk_indices(scores: torch.Tensor, topk: int, lengths: Optional[torch.Tensor] = None,
+                 out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Per query token, the `topk` positions of its fp32 index-score row [T, n] with the
+    highest scores, ascending, -1 padded: int32 [T, topk], the `indices` rows mla_decode takes
+    (one token per row; reshape to [B, s_q, topk]).  lengths (int32 [T]) limits row t to its
+    first lengths[t] positions.  NaN ranks above +inf, -0 equals +0, and ties at the threshold
+    go to the lower positions (dsa_topk_indices in include/dsa_topk.h)."""
+    _need(scores, torch.float32, "scores")
+    if scores.dim() != 2 or scores.stride(1) != 1:
+        raise ValueError("scores must be [T, n] fp32 with a dense last dim")
+    T, n = scores.shape
+    stride = scores.stride(0) if T > 1 else ((n + 3) // 4) * 4
+    # rows are read in 16-byte pieces up to n rounded up to 4: that much must lie in storage
+    need = (T - 1) * stride + ((n + 3) // 4) * 4 if T else 0
+    have = scores.untyped_storage().nbytes() // 4 - scores.storage_offset()
+    if T and (stride % 4 or need > have):
+        raise ValueError("scores rows must have a stride that is a multiple of 4 and be readable "
+                         "up to n rounded up to a multiple of 4")
+    if lengths is not None:
+        _need(lengths, torch.int32, "lengths")
+        if lengths.numel() != T or not lengths.is_contiguous():
+            raise ValueError("lengths must be a contiguous int32 [T]")
+    if out is None:
+        out = torch.empty((T, topk), dtype=torch.int32, device=scores.device)
+    _need(out, torch.int32, "out")
+    if out.dim() != 2 or out.shape[0] != T or out.shape[1] < topk or out.stride(1) != 1:
+        raise ValueError("out must be int32 [T, >= topk] with a dense last dim")
+    check(load_library().dsa_topk_indices(_ptr(scores), stride, _ptr(lengths), T, n, int(topk),
+                                          _ptr(out), out.stride(0), _stream(stream)), "dsa_topk_indices")
+    return out
+
+
 def mla_prefill_v4_fp8(q_nope: torch.Tensor, q_rope: torch.Tensor, unified_kv_nope: torch.Tensor,
                        unified_kv_rope: torch.Tensor, kv_nope: torch.Tensor, kv_rope: torch.Tensor,
                        attn_sink: Optional[torch.Tensor], kv_indptr_prefix: torch.Tensor,

@@ -116,6 +116,34 @@ def dequant_rows_656(rows: np.ndarray) -> np.ndarray:
     return out
 
 
+# ------------------------------------------------------------- top-k selection
+
+def order_keys(x: np.ndarray) -> np.ndarray:
+    """uint32 keys that order fp32 scores as IEEE values, every NaN above +inf and -0 equal
+    to +0 (the order of dsa_topk_indices, include/dsa_topk.h).  The reference has no top-k
+    step: its kernels take the caller's lists (opus_attn/dsa_v4/README.md:185)."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    mag = b & np.uint32(0x7FFFFFFF)
+    key = np.where(b >> np.uint32(31) != 0, ~b, b | np.uint32(0x80000000)).astype(np.uint32)
+    key = np.where(mag == 0, np.uint32(0x80000000), key)
+    return np.where(mag > np.uint32(0x7F800000), np.uint32(0xFFFFFFFF), key).astype(np.uint32)
+
+
+def topk_indices(scores: np.ndarray, lengths, topk: int) -> np.ndarray:
+    """Per row t, the topk positions of scores[t, :lengths[t]] with the highest keys (ties:
+    lower position first), ascending, then -1 up to topk: int32 [T, topk].  These rows are
+    the `indices` the decode path reads (-1 = padding)."""
+    T, n_max = scores.shape
+    out = np.full((T, topk), -1, np.int32)
+    for t in range(T):
+        n = n_max if lengths is None else int(min(max(int(lengths[t]), 0), n_max))
+        key = order_keys(scores[t, :n]).astype(np.int64)
+        order = np.lexsort((np.arange(n), -key))      # key descending, then position ascending
+        sel = np.sort(order[:topk])
+        out[t, :sel.size] = sel
+    return out
+
+
 # ------------------------------------------------------------- attention
 
 def _decode_args(q, kv, fmt, indices, seq_lens, block_table, block_size, kv_batch_stride, causal,
