@@ -10,8 +10,9 @@ also carries config 5 (bf16 sparse prefill, 8192 x 128 heads x top-k 2048) in
 TFLOP/s, the same decode on MXFP8 split streams (the reference's own -dtype fp8
 format, C3-shaped: B=128, s_q=2, 2048 rows per token), the DeepSeek-V4
 prefill (bf16 and fp8 rows) at the reference harness's default shape, the
-dominant kernel's roofline for each, and the CPU oracle timed on a bounded
-sample of each workload on this host.
+top-k index selection that produces config 3's lists (256 tokens, lengths up to
+65536, top-k 2048), the dominant kernel's roofline for each, and the CPU oracle
+timed on a bounded sample of each workload on this host.
 
 Warm-up: by default at least 10 steps and 0.15 s of back-to-back calls per
 workload before the timed steps (the GPU takes tens of ms of sustained load to
@@ -21,6 +22,7 @@ reports the warm-up step count used.
 Algorithmic work (V = valid (query, index) pairs):
   FLOPs = 2 * 128 * (576 + 512) * V
   bytes = Q + V * row_bytes + O + LSE + indices   (row_bytes 656 fp8 / 1152 bf16)
+  top-k selection: bytes = 4 * (sum of row lengths) + 4 * tokens * top-k
 """
 from __future__ import annotations
 
@@ -59,6 +61,9 @@ CONFIGS = {
     # queries, 1024 scattered prefix rows of 65536 pages plus a 128-row extend window, D=512
     "v4": dict(kind="v4", N=4096, topk=1024, pages=65536, window=128, fp8=False),
     "v4fp8": dict(kind="v4", N=4096, topk=1024, pages=65536, window=128, fp8=True),
+    # top-k index selection producing the c3 step's lists: 256 query tokens (B=128, s_q=2),
+    # causal lengths n - s_q + j + 1; five score sets (320 MB) alternate, above the 256 MB MALL
+    "topk": dict(kind="topk", T=256, n=65536, s_q=2, topk=2048, sets=5),
 }
 NAMES = {
     "c1": "bf16 sparse MLA decode B=2 H=128 top-k 2048 (256 pad) flat KV 8192",
@@ -72,6 +77,8 @@ NAMES = {
     "v4": "DeepSeek-V4 bf16 prefill N=4096 H=128 D=512, top-k 1024 of 65536 pages + window 128, sink",
     "v4fp8": ("DeepSeek-V4 fp8 prefill (448 e4m3 + 14 E8M0 | 64 bf16) N=4096 H=128, top-k 1024 of "
               "65536 pages + window 128, sink"),
+    "topk": ("top-k index selection for the c3 step: 256 query tokens (B=128 s_q=2), fp32 scores, "
+             "causal lengths up to 65536, top-k 2048 (5 score sets alternate step by step)"),
 }
 
 
@@ -384,6 +391,51 @@ def cpu_baseline_v4(v, sample):
                 sample=f"{n} of {N} queries ({rows} rows), {dt:.2f} s")
 
 
+def make_topk(cfg, dev, seed=2061):
+    """Index-score rows for the top-k leg: `sets` tensors fp32 [T, n] ~ N(0, 1), the causal
+    lengths of a B x s_q decode step, and the int32 [T, topk] output."""
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    T, n, s_q = cfg["T"], cfg["n"], cfg["s_q"]
+    sets = [torch.randn((T, n), generator=g, device=dev, dtype=torch.float32) for _ in range(cfg["sets"])]
+    lengths = torch.tensor([n - s_q + (t % s_q) + 1 for t in range(T)], dtype=torch.int32, device=dev)
+    out = torch.empty((T, cfg["topk"]), dtype=torch.int32, device=dev)
+    return dict(T=T, n=n, topk=cfg["topk"], sets=sets, lengths=lengths, out=out)
+
+
+def topk_step(tk):
+    """One selection call per step through the C ABI, arguments built once; the score sets
+    alternate step by step."""
+    import torch
+    from opfoundry_amd.abi import check, load_library
+    f = load_library().dsa_topk_indices
+    stream = torch.cuda.current_stream().cuda_stream
+    args = [(x.data_ptr(), tk["n"], tk["lengths"].data_ptr(), tk["T"], tk["n"], tk["topk"],
+             tk["out"].data_ptr(), tk["topk"], stream) for x in tk["sets"]]
+    state = [0]
+
+    def step():
+        a = args[state[0] % len(args)]
+        state[0] += 1
+        rc = f(*a)
+        if rc:
+            check(rc, "dsa_topk_indices")
+    return step
+
+
+def cpu_baseline_topk(tk, sample):
+    """numpy oracle (one core) on the first `sample` tokens of one score set, scaled to the step."""
+    import oracle
+    n_s = min(sample, tk["T"])
+    scores = tk["sets"][0][:n_s].cpu().numpy()
+    lengths = tk["lengths"][:n_s].cpu().numpy()
+    t0 = time.perf_counter()
+    oracle.topk_indices(scores, lengths, tk["topk"])
+    dt = time.perf_counter() - t0
+    return dict(value=round(dt / n_s * tk["T"] * 1e6, 1), unit="us/step", cores=1, kind="port",
+                sample=f"{n_s} of {tk['T']} tokens, {dt:.2f} s, scaled to the step")
+
+
 def measured_peaks(dev):
     """Achievable rates on this GPU, beside the spec peaks: a STREAM-like 2 GiB device copy
     (read + write bytes / time) and a large dense bf16 GEMM through torch (hipBLASLt)."""
@@ -598,6 +650,9 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-mx", action="store_true")
     ap.add_argument("--no-v4", action="store_true")
+    ap.add_argument("--no-topk", action="store_true")
+    ap.add_argument("--cpu-topk-sample", type=int, default=64,
+                    help="query tokens of the topk step the CPU oracle runs")
     ap.add_argument("--no-peaks", action="store_true")
     ap.add_argument("--cpu-v4-sample", type=int, default=128,
                     help="V4 prefill queries the CPU oracle runs")
@@ -639,6 +694,14 @@ def main():
         log(f"building {args.config} inputs")
         v = make_v4(cfg, dev)
         ms = time_steps(v4_step(v, dev)[0], args.steps, args.warmup)
+        print(json.dumps({"config": args.config, "ms_per_step": ms}))
+        return
+    if cfg["kind"] == "topk":
+        if not args.kernel_only:
+            ap.error("--config topk is reported inside the default JSON line; use it with --kernel-only")
+        log("building topk inputs")
+        tk = make_topk(cfg, dev)
+        ms = time_steps(topk_step(tk), args.steps, args.warmup)
         print(json.dumps({"config": args.config, "ms_per_step": ms}))
         return
     if cfg["kind"] == "mxfp8":
@@ -782,6 +845,27 @@ def main():
             del v, vstep
             torch.cuda.empty_cache()
 
+    if not args.no_topk:
+        log("building topk inputs")
+        tk = make_topk(CONFIGS["topk"], dev)
+        tstep = topk_step(tk)
+        tms = time_steps(tstep, args.steps, args.warmup)
+        tk_ms = kernel_avg_ms(tstep, max(10, args.steps))
+        t_bytes = 4 * int(tk["lengths"].sum().item()) + 4 * tk["T"] * tk["topk"]
+        tach = t_bytes / (tk_ms * 1e-3) / 1e9
+        res["topk"] = {"workload": f"topk: {NAMES['topk']}", "us_per_step": round(tms * 1e3, 3),
+                       "dtype": "fp32 scores -> int32 positions",
+                       "roofline": {"bound": "hbm", "achieved": round(tach, 1), "peak": HBM_PEAK_GBS,
+                                    "unit": "GB/s", "frac": round(tach / HBM_PEAK_GBS, 4),
+                                    "traffic": profiled_traffic("dsa_topk_traffic.txt"),
+                                    "kernel": "dsa_topk_kernel", "kernel_avg_us": round(tk_ms * 1e3, 3),
+                                    "alg_bytes": t_bytes}}
+        if not args.no_cpu:
+            log("CPU baseline (oracle) on a topk sample")
+            res["topk"]["cpu_baseline"] = cpu_baseline_topk(tk, args.cpu_topk_sample)
+        del tk, tstep
+        torch.cuda.empty_cache()
+
     if not args.no_prefill:
         log("building c5 prefill inputs")
         p = make_prefill(CONFIGS["c5"], dev)
@@ -808,9 +892,10 @@ def main():
         res["measured_peaks"] = pk
         # fractions against the achievable rates beside the spec ones
         res["roofline"]["frac_measured"] = round(res["roofline"]["achieved"] / pk["hbm_copy_GBps"], 4)
-        if "mxfp8" in res:
-            r = res["mxfp8"]["roofline"]
-            r["frac_measured"] = round(r["achieved"] / pk["hbm_copy_GBps"], 4)
+        for key in ("mxfp8", "topk"):
+            if key in res:
+                r = res[key]["roofline"]
+                r["frac_measured"] = round(r["achieved"] / pk["hbm_copy_GBps"], 4)
         for leg in [res.get("prefill")] + list(res.get("v4_prefill", {}).values()):
             if leg:
                 leg["roofline"]["frac_measured"] = round(leg["roofline"]["achieved"] / pk["bf16_gemm_TFLOPs"], 4)

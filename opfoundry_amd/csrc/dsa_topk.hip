@@ -31,7 +31,8 @@ constexpr int TK_THREADS = 1024;
 constexpr int TK_WAVES = TK_THREADS / 64;
 constexpr int TK_FIRST_BITS = 12;          // first histogram: 4096 bins
 constexpr int TK_NEXT_BITS = 10;           // refinement passes: 1024 bins
-constexpr int TK_UNROLL = 4;               // float4 loads in flight per lane in a histogram pass
+constexpr int TK_UNROLL = 8;               // float4 loads in flight per lane in a histogram pass
+constexpr int TK_GROUP = 4;                // compaction: segments of 4096 positions loaded together
 
 // Order-preserving key: a > b as scores <=> key(a) > key(b) as uint32.  Every
 // NaN maps to the largest key, and -0 to the key of +0.
@@ -161,40 +162,61 @@ __global__ __launch_bounds__(TK_THREADS) void dsa_topk_kernel(
     // position's slot is the number of taken positions before it.
     const uint32_t r_eff = take_all ? 0xffffffffu : r;
     uint32_t run_gt = 0, run_eq = 0;
-    for (int base = 0; base < n4; base += TK_THREADS) {
-        const int i = base + tid;
-        uint32_t flags = 0;  // bit c: above; bit 4 + c: equal
-        if (i < n4) {
-            const float4 v = row[i];
-            const float e[4] = {v.x, v.y, v.z, v.w};
+    // Segments of 4096 positions are loaded TK_GROUP at a time, and the next group's
+    // loads are issued before this group's scans, so the scans' barriers overlap the
+    // memory latency instead of waiting on one load each.
+    float4 cur[TK_GROUP], nxt[TK_GROUP];
+#pragma unroll
+    for (int j = 0; j < TK_GROUP; ++j) {
+        const int i = j * TK_THREADS + tid;
+        if (i < n4) cur[j] = row[i];
+    }
+    for (int gbase = 0; gbase < n4; gbase += TK_GROUP * TK_THREADS) {
+        const int gnext = gbase + TK_GROUP * TK_THREADS;
+#pragma unroll
+        for (int j = 0; j < TK_GROUP; ++j) {
+            const int i = gnext + j * TK_THREADS + tid;
+            if (i < n4) nxt[j] = row[i];
+        }
+#pragma unroll
+        for (int j = 0; j < TK_GROUP; ++j) {
+            const int sbase = gbase + j * TK_THREADS;
+            if (sbase >= n4) break;  // uniform: the same for every thread
+            const int i = sbase + tid;
+            uint32_t flags = 0;      // bit c: above; bit 4 + c: equal
+            if (i < n4) {
+                const float e[4] = {cur[j].x, cur[j].y, cur[j].z, cur[j].w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    if (4 * i + c >= n) continue;
+                    const uint32_t top = key_top(order_key(e[c]), L);
+                    if (top > P) flags |= 1u << c;
+                    else if (top == P) flags |= 16u << c;
+                }
+            }
+            const uint32_t mine = (uint32_t)__builtin_popcount(flags & 15u) |
+                                  ((uint32_t)__builtin_popcount(flags >> 4) << 16);
+            uint32_t tot;
+            const uint32_t ex = wg_scan(mine, part, &tot) - mine;
+            uint32_t gb = run_gt + (ex & 0xffffu), eb = run_eq + (ex >> 16);
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                if (4 * i + c >= n) continue;
-                const uint32_t top = key_top(order_key(e[c]), L);
-                if (top > P) flags |= 1u << c;
-                else if (top == P) flags |= 16u << c;
+                // slots stay below k when the row is not modified during the call; the
+                // bound check keeps a caller's race on `scores` from writing past the row
+                if ((flags >> c) & 1u) {
+                    const uint32_t slot = gb + (eb < r_eff ? eb : r_eff);
+                    if (slot < (uint32_t)k) out[slot] = 4 * i + c;
+                    ++gb;
+                } else if ((flags >> (4 + c)) & 1u) {
+                    if (eb < r_eff && gb + eb < (uint32_t)k) out[gb + eb] = 4 * i + c;
+                    ++eb;
+                }
             }
+            run_gt += tot & 0xffffu;
+            run_eq += tot >> 16;
         }
-        const uint32_t mine = (uint32_t)__builtin_popcount(flags & 15u) |
-                              ((uint32_t)__builtin_popcount(flags >> 4) << 16);
-        uint32_t tot;
-        const uint32_t ex = wg_scan(mine, part, &tot) - mine;
-        uint32_t gb = run_gt + (ex & 0xffffu), eb = run_eq + (ex >> 16);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            // slots stay below k when the row is not modified during the call; the
-            // bound check keeps a caller's race on `scores` from writing past the row
-            if ((flags >> c) & 1u) {
-                const uint32_t slot = gb + (eb < r_eff ? eb : r_eff);
-                if (slot < (uint32_t)k) out[slot] = 4 * i + c;
-                ++gb;
-            } else if ((flags >> (4 + c)) & 1u) {
-                if (eb < r_eff && gb + eb < (uint32_t)k) out[gb + eb] = 4 * i + c;
-                ++eb;
-            }
-        }
-        run_gt += tot & 0xffffu;
-        run_eq += tot >> 16;
+        for (int j = 0; j < TK_GROUP; ++j) cur[j] = nxt[j];
     }
     const uint32_t taken = run_gt + (run_eq < r_eff ? run_eq : r_eff);
     for (uint32_t j = taken + (uint32_t)tid; j < (uint32_t)k; j += TK_THREADS) out[j] = -1;

@@ -27,6 +27,7 @@ LEGS = {
     "dsa_mla_fwd_bf16_c5_traffic.txt": 2_362_441_728,
     "dsa_mla_fwd_v4_traffic.txt": None,
     "dsa_mla_fwd_v4fp8_traffic.txt": None,
+    "dsa_topk_traffic.txt": 69_205_504,
 }
 
 
