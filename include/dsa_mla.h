@@ -83,7 +83,10 @@ enum {
 /*
  * Sparse MLA decode, top-k form.
  * q       : bf16 [B, s_q, H, 576] addressed by q_stride_{b,t,h} (last dim dense)
- * kv_cache: [kv_total_rows, row] in kv_format; rows are block_size-row pages
+ * kv_cache: [kv_total_rows, row] in kv_format; rows are block_size-row pages,
+ *           kv_stride_row elements apart (bf16 elements for DSA_KV_BF16 rows,
+ *           bytes for DSA_KV_FP8_656 rows; 0 = dense rows of 576 / 656).  A
+ *           row stride is at least one row and a multiple of 16 bytes.
  * out     : bf16 [B, s_q, H, 512] addressed by o_stride_{b,t,h}
  * lse     : fp32 [B, s_q, H] dense (may be NULL)
  * num_splits: 0 = automatic; otherwise 1..DSA_MLA_MAX_SPLITS.  With more than
@@ -100,6 +103,7 @@ typedef struct {
     int32_t kv_format;
     int32_t block_size;
     int64_t kv_batch_stride;
+    int64_t kv_stride_row;       /* 0 = dense rows */
 
     const int32_t* block_table;
     int64_t block_table_stride;
@@ -163,7 +167,12 @@ int dsa_mla_combine(const float* partial_o, const float* partial_lse, int32_t nu
  * q        : bf16 [B * s_q, H, 576]; query row i = b * s_q + t at
  *            q + i * stride_q_b + h * stride_q_h (elements)
  * kv       : [total_tokens, row] in kv_format; page size 1, so an index is a
- *            physical cache row (bf16 rows are 576 elements apart)
+ *            physical cache row.  Rows are stride_kv_page elements apart
+ *            (defs.h:129, "the row stride of the latent KV tensor",
+ *            opus_attn/dsa_v32/README.md:99): bf16 elements for DSA_KV_BF16
+ *            rows (the reference harness passes 576), bytes for
+ *            DSA_KV_FP8_656 rows; 0 = dense rows.  A row stride is at least
+ *            one row and a multiple of 16 bytes.
  * kv_indptr: int32 [B + 1]; kv_indices: int32 rows.  Query token t of batch b
  *            attends kv_indices[kv_indptr[b] + p] for
  *            0 <= p < kv_indptr[b + 1] - kv_indptr[b] - (s_q - 1 - t)
@@ -173,7 +182,9 @@ int dsa_mla_combine(const float* partial_o, const float* partial_lse, int32_t nu
  * out      : bf16 [B * s_q, H, 512] at out + i * stride_o_b + h * stride_o_h
  * lse      : fp32 [B * s_q, H] dense (may be NULL)
  * max_kv_len: an upper bound of kv_indptr[b + 1] - kv_indptr[b] over b (the
- *            host cannot read the device lists; the split plan uses it)
+ *            host cannot read the device lists; the split plan uses it).  A
+ *            query whose list is longer is not truncated silently: its O and
+ *            LSE are NaN.
  */
 typedef struct {
     const void* q;
@@ -186,6 +197,7 @@ typedef struct {
     int32_t total_tokens;
     int32_t stride_q_b, stride_q_h;
     int32_t stride_o_b, stride_o_h;
+    int32_t stride_kv_page;      /* 0 = dense rows */
     int32_t kv_format;
     int32_t max_kv_len;
     int32_t num_splits;          /* 0 = automatic */
@@ -255,7 +267,8 @@ int dsa_mla_decode_mxfp8(const dsa_mla_decode_mxfp8_args* args, void* workspace,
 /*
  * Sparse MLA prefill (per-query top-k over one KV pool).
  * q       : bf16 [N, H, 576] addressed by q_stride_{n,h}
- * kv      : [kv_rows, row] in kv_format
+ * kv      : [kv_rows, row] in kv_format, rows kv_stride_row elements apart
+ *           (as in dsa_mla_decode_args; 0 = dense)
  * indices : int32 [N, topk] (row stride idx_stride_n); entry j of query i is
  *           valid iff 0 <= j < kv_rows and, when causal != 0,
  *           j <= i + causal_offset
@@ -268,6 +281,7 @@ typedef struct {
     int64_t q_stride_n, q_stride_h;
     const void* kv;
     int64_t kv_rows;
+    int64_t kv_stride_row;       /* 0 = dense rows */
     int32_t kv_format;
     const int32_t* indices;
     int64_t idx_stride_n;
@@ -298,8 +312,10 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* args, void* workspace, size_t wo
  * stride_kv_page elements apart.  A row outside its pool is skipped; a query
  * with no rows gets O = 0 (and LSE = +inf).  lse (an addition to the
  * reference, may be NULL) is the natural log of the denominator, sink
- * included.  max_rows bounds the prefix + extend rows of any query and must be
- * <= 2048; H must be 128.
+ * included.  max_rows bounds the prefix + extend entries of any query and
+ * must be <= 2048 (a query with more gets NaN O and LSE, never a silently
+ * truncated attention); H must be 128; total_pages and total_tokens must be
+ * below 2^30.
  */
 typedef struct {
     const void* q;

@@ -56,7 +56,7 @@ EXPORTED_SYMBOLS = (
     "dsa_mla_abi_version",
 )
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -69,7 +69,7 @@ class DecodeArgs(ctypes.Structure):
     _fields_ = [
         ("q", _vp), ("q_stride_b", _i64), ("q_stride_t", _i64), ("q_stride_h", _i64),
         ("kv_cache", _vp), ("kv_total_rows", _i64), ("kv_format", _i32), ("block_size", _i32),
-        ("kv_batch_stride", _i64),
+        ("kv_batch_stride", _i64), ("kv_stride_row", _i64),
         ("block_table", _vp), ("block_table_stride", _i64),
         ("seq_lens", _vp),
         ("indices", _vp), ("idx_stride_b", _i64), ("idx_stride_t", _i64),
@@ -88,6 +88,7 @@ class CsrArgs(ctypes.Structure):
         ("kv_indptr", _vp), ("kv_indices", _vp),
         ("B", _i32), ("s_q", _i32), ("H", _i32), ("total_tokens", _i32),
         ("stride_q_b", _i32), ("stride_q_h", _i32), ("stride_o_b", _i32), ("stride_o_h", _i32),
+        ("stride_kv_page", _i32),
         ("kv_format", _i32), ("max_kv_len", _i32), ("num_splits", _i32),
         ("softmax_scale", ctypes.c_float),
     ]
@@ -117,7 +118,7 @@ class PrefillArgs(ctypes.Structure):
 
     _fields_ = [
         ("q", _vp), ("q_stride_n", _i64), ("q_stride_h", _i64),
-        ("kv", _vp), ("kv_rows", _i64), ("kv_format", _i32),
+        ("kv", _vp), ("kv_rows", _i64), ("kv_stride_row", _i64), ("kv_format", _i32),
         ("indices", _vp), ("idx_stride_n", _i64),
         ("out", _vp), ("o_stride_n", _i64), ("o_stride_h", _i64),
         ("lse", _vp),

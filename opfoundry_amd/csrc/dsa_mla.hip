@@ -34,6 +34,7 @@
 #include <type_traits>
 
 #include "../../include/dsa_mla.h"
+#include "dsa_rows.h"
 
 namespace {
 
@@ -71,7 +72,7 @@ constexpr int RAW_STRIDE = FP8_LOADS * 1024;         // raw slot padded to whole
 constexpr int FP8_LPW = (FP8_LOADS + NWAVE - 1) / NWAVE;  // loads of wave 0 (6); the others 5
 constexpr int BF16_LPW = TILE / NWAVE + 1;           // 8 NoPE rows + one 8-row RoPE block
 constexpr int FP8_SCALE_OFF = D_NOPE;                // 4 fp32 scales
-constexpr int32_t POOL2 = 1 << 30;                   // row-list tag: a row of the second pool (V4 extend)
+constexpr int32_t POOL2 = dsa_rows::POOL2;           // row-list tag: a row of the second pool (V4 extend)
 constexpr int FP8_ROPE_OFF = D_NOPE + 16;            // 64 bf16 RoPE values
 // MXFP8 raw slot, one region per stream (every DMA load reads one stream):
 // NoPE codes of row r at 512 r (loads 0..15, two rows each), RoPE at
@@ -229,7 +230,7 @@ struct FwdParams {
     const int32_t* idx_ext;
     const unsigned char* kv2;    // second row pool (V4 extend rows)
     int64_t kv2_rows;
-    int64_t row_bytes;           // bytes between cache rows (512-value rows)
+    int64_t row_bytes;           // bytes between cache rows (bf16, 656-B and 512-value rows)
     const float* attn_sink;      // per-head sink in the softmax denominator, or NULL
     // MXFP8 split streams: q carries the bf16 RoPE part of Q, kv the fp8 NoPE
     // codes; strides of the fp8 / E8M0 streams in bytes
@@ -255,18 +256,8 @@ struct FwdParams {
 
 // Physical cache row of logical position j of query (b, t); -1 if invalid.
 __device__ __forceinline__ int64_t resolve_row(const FwdParams& p, int b, int64_t jmax, int32_t j) {
-    if (j < 0 || (int64_t)j >= jmax) return -1;
-    int64_t row;
-    if (p.block_table) {
-        const int32_t blk_i = p.bs_shift >= 0 ? (j >> p.bs_shift) : (j / p.block_size);
-        const int32_t in_blk = p.bs_shift >= 0 ? (j & (p.block_size - 1)) : (j % p.block_size);
-        const int32_t blk = p.block_table[(int64_t)b * p.bt_stride + blk_i];
-        row = (int64_t)blk * p.block_size + in_blk;
-    } else {
-        row = (int64_t)b * p.kv_batch_stride + j;
-    }
-    if (row < 0 || row >= p.kv_total_rows) return -1;
-    return row;
+    return dsa_rows::topk_row(j, jmax, p.block_table ? p.block_table + (int64_t)b * p.bt_stride : nullptr,
+                              p.block_size, p.bs_shift, (int64_t)b * p.kv_batch_stride, p.kv_total_rows);
 }
 
 // One piece of the fp8 dequant in flight: codes + scale, or 16 RoPE bytes.
@@ -317,6 +308,23 @@ __device__ __forceinline__ u32x4 mx_to_bf16(unsigned c0, unsigned c1, unsigned e
                  __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)c0, sf, true)),
                  __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)c1, sf, false)),
                  __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)c1, sf, true))};
+}
+
+// The attention sink joins the softmax denominator as exp(sink), with the
+// maximum taken over the scores and the sink together (mla_v4_host.cc:469-472).
+// In log2 units: the rows' sum l_rows is taken against reference m; the result
+// is the denominator l_out against reference m_out = max(m, sink2), so a sink
+// far above every score (or far below) neither overflows nor underflows the
+// sum.  O then scales by 2^(m - m_out) / l_out, and LSE = m_out + log2 l_out.
+__device__ __forceinline__ void add_sink(float l_rows, float m, float sink2, float& l_out, float& m_out) {
+    const float d = sink2 - m;
+    if (d > 0.0f) {
+        l_out = __builtin_fmaf(l_rows, __builtin_amdgcn_exp2f(-d), 1.0f);
+        m_out = sink2;
+    } else {
+        l_out = l_rows + __builtin_amdgcn_exp2f(d);
+        m_out = m;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -393,6 +401,9 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     int64_t jmax = 0;
     const int32_t* idx;
     int64_t v4_np = 0, v4_eb = 0;
+    // the splits of a query cover gridDim.z * chunk entries of its list
+    const int64_t k_cap = (int64_t)gridDim.z * p.chunk;
+    bool truncated = false;
     if (L::D512 && p.ind_pre) {
         // V4: prefix rows of kv, then extend rows of kv2 (tagged with POOL2);
         // a decreasing indptr pair counts as an empty range
@@ -401,11 +412,13 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         v4_eb = p.ind_ext[b];
         const int64_t ne = max((int64_t)p.ind_ext[b + 1] - v4_eb, (int64_t)0);
         k1 = (int)min((int64_t)k0 + p.chunk, v4_np + ne);
+        truncated = v4_np + ne > k_cap;
         idx = p.idx_pre + pb;
     } else if (p.kv_indptr) {
         const int64_t kb = p.kv_indptr[b];
         const int64_t count = (int64_t)p.kv_indptr[b + 1] - kb - (p.s_q - 1 - t);
         k1 = (int)min((int64_t)k0 + p.chunk, count);
+        truncated = count > k_cap;
         idx = p.kv_indices + kb;
     } else {
         k1 = min(k0 + p.chunk, p.topk);
@@ -420,23 +433,24 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     int32_t rows_local[PER_T];
     int cnt = 0;
     {
+        // all loads first (they overlap), then the rules of dsa_rows.h; a V4
+        // entry is checked against the pool its list names (ext[e])
         int32_t jv[PER_T];
+        bool ext[PER_T];
 #pragma unroll
         for (int e = 0; e < PER_T; ++e) {
             const int k = k0 + tid * PER_T + e;
-            if (L::D512 && p.ind_pre && k < k1 && k >= v4_np) {
-                const int32_t j = p.idx_ext[v4_eb + (k - v4_np)];
-                jv[e] = j >= 0 && (int64_t)j < p.kv2_rows ? (j | POOL2) : -1;
-            } else {
-                jv[e] = k < k1 ? idx[k] : -1;
-            }
+            ext[e] = L::D512 && p.ind_pre && k >= v4_np;
+            if (k >= k1) jv[e] = -1;
+            else jv[e] = ext[e] ? p.idx_ext[v4_eb + (k - v4_np)] : idx[k];
         }
 #pragma unroll
         for (int e = 0; e < PER_T; ++e) {
-            if (L::D512 && p.ind_pre)   // extend ids were checked above; prefix ids against kv
-                rows_local[e] = (jv[e] & POOL2) ? jv[e] : (jv[e] >= 0 && (int64_t)jv[e] < p.kv_total_rows ? jv[e] : -1);
+            if (L::D512 && p.ind_pre)
+                rows_local[e] = ext[e] ? dsa_rows::v4_extend_row(jv[e], p.kv2_rows)
+                                       : dsa_rows::v4_prefix_row(jv[e], p.kv_total_rows);
             else
-                rows_local[e] = p.kv_indptr ? (jv[e] >= 0 && (int64_t)jv[e] < p.kv_total_rows ? jv[e] : -1)
+                rows_local[e] = p.kv_indptr ? dsa_rows::csr_row(jv[e], p.kv_total_rows)
                                             : (int32_t)resolve_row(p, b, jmax, jv[e]);
             cnt += rows_local[e] >= 0 ? 1 : 0;
         }
@@ -540,15 +554,15 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                 const unsigned char* base;
                 if constexpr (L::D512) {
                     const int32_t id = g.r[i];
-                    base = ((id & POOL2) ? p.kv2 : p.kv) + (int64_t)(id & (POOL2 - 1)) * p.row_bytes;
+                    base = (dsa_rows::row_in_pool2(id) ? p.kv2 : p.kv) + (int64_t)dsa_rows::row_index(id) * p.row_bytes;
                 } else {
-                    base = p.kv + (int64_t)g.r[i] * BF16_ROW;
+                    base = p.kv + (int64_t)g.r[i] * p.row_bytes;
                 }
                 lds_dma16_s(base, 16u * (unsigned)(ln ^ nope_sw(r)), tb + r * NOPE_STRIDE);
             } else if constexpr (!L::D512) {
                 const int r = 8 * wave + (ln >> 3);
                 const unsigned char* src =
-                    p.kv + (int64_t)g.rope * BF16_ROW + 2 * D_NOPE + 16 * ((ln & 7) ^ rope_sw(r));
+                    p.kv + (int64_t)g.rope * p.row_bytes + 2 * D_NOPE + 16 * ((ln & 7) ^ rope_sw(r));
                 lds_dma16(src, tb + ROPE_OFF + 8 * wave * 128);
             }
         } else {
@@ -571,8 +585,8 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                     const unsigned char* q0 = p.kv_ro;
                     const unsigned char* q1 = p.kv2_ro;
                     asm("" : "+s"(n0), "+s"(n1), "+s"(q0), "+s"(q1));
-                    const bool e2 = (g.r[i] & POOL2) != 0;
-                    const uint64_t r64 = (uint32_t)(g.r[i] & (POOL2 - 1));
+                    const bool e2 = dsa_rows::row_in_pool2(g.r[i]);
+                    const uint64_t r64 = (uint32_t)dsa_rows::row_index(g.r[i]);
                     const unsigned char* src =
                         k < 16 ? (e2 ? n1 : n0) + r64 * p.kvn_st + 16 * (ln & 31)
                                : (e2 ? q1 : q0) + r64 * p.kvr_st + 16 * (ln & 7);
@@ -584,7 +598,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                                : (k < 20 ? p.kv_ro + row * p.kvr_st + 16 * (ln & 7) : p.kv_sc + row * p.kvs_st);
                     lds_dma16(src, RING + slot * RAW_STRIDE + 1024 * k);
                 } else {
-                    lds_dma16(p.kv + (row * FP8_ROW + ((unsigned)opaque((int)f_rc[i]) >> 16)),
+                    lds_dma16(p.kv + (row * (uint64_t)p.row_bytes + ((unsigned)opaque((int)f_rc[i]) >> 16)),
                               RING + slot * RAW_STRIDE + 1024 * k);
                 }
             }
@@ -855,9 +869,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) lt += __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], c_s, -m_ref));
             lt += __shfl_xor(lt, 32, 64);
+            float m_fold = m_ref;
             if constexpr (L::D512)
-                if (p.attn_sink) lt += __builtin_amdgcn_exp2f(__builtin_fmaf(p.attn_sink[head], LOG2E, -m_ref));
-            m_ref += __builtin_amdgcn_logf(lt);
+                if (p.attn_sink) add_sink(lt, m_ref, p.attn_sink[head] * LOG2E, lt, m_fold);
+            m_ref = m_fold + __builtin_amdgcn_logf(lt);
         }
         // P of both halves, then one barrier: the wave's VALU work does not
         // overlap its own MFMAs, so exponentials placed between the PV MFMAs
@@ -970,9 +985,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) lt += __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c_s, -m_ref));
             lt += __shfl_xor(lt, 32, 64);
+            float m_fold = m_ref;
             if constexpr (L::D512)
-                if (p.attn_sink) lt += __builtin_amdgcn_exp2f(__builtin_fmaf(p.attn_sink[head], LOG2E, -m_ref));
-            m_ref += __builtin_amdgcn_logf(lt);
+                if (p.attn_sink) add_sink(lt, m_ref, p.attn_sink[head] * LOG2E, lt, m_fold);
+            m_ref = m_fold + __builtin_amdgcn_logf(lt);
         }
         float e[16];
 #pragma unroll
@@ -1107,21 +1123,28 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // Wave w holds O for dims 128w..128w+127 of all heads; the softmax sums
     // and references are per head, owned by the head's QK wave: exchange them.
     const float l_rows = l_lane + __shfl_xor(l_lane, 32, 64);
-    const bool has = l_rows > 0.0f;
-    // the softmax denominator: the rows' sum plus an attention sink, exp(sink - m)
+    // rows were attended (their P may all have underflowed under a dominant sink)
+    const bool has = n_valid > 0;
+    // the softmax denominator: the rows' sum plus an attention sink
     // (mla_v4_host.cc:469-472; LSE then covers the sink as well)
-    float l = l_rows;
+    float l = l_rows, m_fin = m_ref, o_scale = 1.0f;
     if constexpr (L::D512)
-        if (p.attn_sink) l += __builtin_amdgcn_exp2f(__builtin_fmaf(p.attn_sink[head], LOG2E, -m_ref));
+        if (p.attn_sink) {
+            add_sink(l_rows, m_ref, p.attn_sink[head] * LOG2E, l, m_fin);
+            o_scale = __builtin_amdgcn_exp2f(m_ref - m_fin);
+        }
     const int64_t qrow = (int64_t)b * p.s_q + t;
     LDS_AS float* const s_l = (LDS_AS float*)PX;      // P buffer is free now
-    if (hi == 0) s_l[head] = has ? (ntiles == 1 ? 1.0f : 1.0f / l) : 0.0f;   // one tile: P is normalised
+    // one tile: P is normalised.  A list longer than the caller's bound
+    // (max_kv_len / max_rows) was cut: its outputs are NaN, never a silently
+    // truncated attention.
+    if (hi == 0) s_l[head] = truncated ? __builtin_nanf("") : (has ? (ntiles == 1 ? 1.0f : o_scale / l) : 0.0f);
     if (hi == 0) {
-        const float lse_v = (m_ref + __builtin_amdgcn_logf(l)) * LN2;
+        const float lse_v = truncated ? __builtin_nanf("") : (m_fin + __builtin_amdgcn_logf(l)) * LN2;
         if (p.part_o == nullptr) {
-            if (p.lse) p.lse[qrow * HEADS + head] = has ? lse_v : INFINITY;
+            if (p.lse) p.lse[qrow * HEADS + head] = has || truncated ? lse_v : INFINITY;
         } else {
-            p.part_lse[((int64_t)split * p.B * p.s_q + qrow) * HEADS + head] = has ? lse_v : -FLT_MAX;
+            p.part_lse[((int64_t)split * p.B * p.s_q + qrow) * HEADS + head] = has || truncated ? lse_v : -FLT_MAX;
         }
     }
     __syncthreads();
@@ -1216,7 +1239,9 @@ dsa_mla_combine_kernel(const float* __restrict__ part_o, const float* __restrict
     float den = 0.0f;
     for (int s = 0; s < ns; ++s) {
         const float ls = part_lse[s * stride + rh];
-        const float w = ls > -FLT_MAX ? __builtin_amdgcn_exp2f((ls - m) * LOG2E) : 0.0f;
+        // an empty split (-FLT_MAX) weighs 0; a NaN LSE (a list cut short)
+        // makes the row NaN
+        const float w = ls > -FLT_MAX || ls != ls ? __builtin_amdgcn_exp2f((ls - m) * LOG2E) : 0.0f;
         den += w;
         const f32x4* src = reinterpret_cast<const f32x4*>(part_o + (s * stride + rh) * D_VO + 8 * lane);
         acc0 += w * src[0];
@@ -1229,7 +1254,7 @@ dsa_mla_combine_kernel(const float* __restrict__ part_o, const float* __restrict
     __bf16* op = out + (int64_t)(row / s_q) * o_sb + (int64_t)(row % s_q) * o_st + (int64_t)head * o_sh + 8 * lane;
     reinterpret_cast<u32x2*>(op)[0] = __builtin_bit_cast(u32x2, b0);
     reinterpret_cast<u32x2*>(op)[1] = __builtin_bit_cast(u32x2, b1);
-    if (lse && lane == 0) lse[rh] = den > 0.0f ? m + __builtin_amdgcn_logf(den) * LN2 : INFINITY;
+    if (lse && lane == 0) lse[rh] = den > 0.0f || den != den ? m + __builtin_amdgcn_logf(den) * LN2 : INFINITY;
 }
 
 // ---------------------------------------------------------------------------
@@ -1298,6 +1323,17 @@ dsa_kv_quantize_kernel(const __bf16* __restrict__ src, int64_t src_stride, int64
 // ------------------------------------------------------------------- host
 
 bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+// Bytes between cache rows for a row stride given in elements of the row
+// format's storage type (bf16 elements, or bytes for 656-B rows); 0 = dense.
+// -1 when the stride is shorter than a row or not a multiple of 16 bytes
+// (every gather load is 16 bytes).
+int64_t row_stride_bytes(int fmt, int64_t stride) {
+    const int64_t dense = fmt == DSA_KV_FP8_656 ? FP8_ROW : BF16_ROW;
+    if (stride == 0) return dense;
+    const int64_t bytes = fmt == DSA_KV_FP8_656 ? stride : 2 * stride;
+    return stride < 0 || bytes < dense || (bytes % 16) != 0 ? -1 : bytes;
+}
 int ilog2(int v) { int s = 0; while ((1 << s) < v) ++s; return s; }
 
 int auto_splits(int64_t queries, int topk) {
@@ -1319,6 +1355,7 @@ int validate_decode(const dsa_mla_decode_args* a, int* ns_out, int* chunk_out) {
     if (a->kv_format != DSA_KV_BF16 && a->kv_format != DSA_KV_FP8_656) return DSA_ERR_BAD_FORMAT;
     if (a->kv_total_rows < 0 || a->kv_total_rows > INT32_MAX) return DSA_ERR_BAD_SHAPE;
     if (a->block_table && a->block_size <= 0) return DSA_ERR_BAD_SHAPE;
+    if (row_stride_bytes(a->kv_format, a->kv_stride_row) < 0) return DSA_ERR_BAD_STRIDE;
     if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
     const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q, a->topk);
     const int chunk = a->topk == 0 ? 0 : (a->topk + ns - 1) / ns;
@@ -1369,6 +1406,7 @@ int validate_csr(const dsa_mla_decode_csr_args* a, int* ns_out, int* chunk_out) 
     if (a->B < 0 || a->s_q <= 0 || a->max_kv_len < 0 || a->total_tokens < 0) return DSA_ERR_BAD_SHAPE;
     if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
     if (a->kv_format != DSA_KV_BF16 && a->kv_format != DSA_KV_FP8_656) return DSA_ERR_BAD_FORMAT;
+    if (row_stride_bytes(a->kv_format, a->stride_kv_page) < 0) return DSA_ERR_BAD_STRIDE;
     if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
     const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q, a->max_kv_len);
     const int chunk = a->max_kv_len == 0 ? 0 : (a->max_kv_len + ns - 1) / ns;
@@ -1429,7 +1467,7 @@ size_t mx_ws_bytes(const dsa_mla_decode_mxfp8_args* a, int ns) {
 
 extern "C" {
 
-int dsa_mla_abi_version(void) { return 5; }
+int dsa_mla_abi_version(void) { return 6; }
 
 const char* dsa_mla_strerror(int code) {
     switch (code) {
@@ -1478,6 +1516,7 @@ int dsa_mla_decode(const dsa_mla_decode_args* a, void* ws, size_t ws_bytes, void
     fp.kv = (const unsigned char*)a->kv_cache;
     fp.kv_total_rows = a->kv_total_rows;
     fp.kv_batch_stride = a->kv_batch_stride;
+    fp.row_bytes = row_stride_bytes(a->kv_format, a->kv_stride_row);
     fp.block_table = a->block_table;
     fp.bt_stride = a->block_table_stride;
     fp.block_size = a->block_table ? a->block_size : 1;
@@ -1525,6 +1564,7 @@ int dsa_mla_decode_csr(const dsa_mla_decode_csr_args* a, void* ws, size_t ws_byt
     fp.q_sb = (int64_t)a->s_q * a->stride_q_b; fp.q_st = a->stride_q_b; fp.q_sh = a->stride_q_h;
     fp.kv = (const unsigned char*)a->kv;
     fp.kv_total_rows = a->total_tokens;
+    fp.row_bytes = row_stride_bytes(a->kv_format, a->stride_kv_page);
     fp.block_size = 1;
     fp.seq_len_default = a->total_tokens;
     fp.kv_indptr = a->kv_indptr;
@@ -1619,6 +1659,7 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* a, void* ws, size_t ws_bytes, vo
     if (a->N < 0 || a->topk < 0 || a->kv_rows < 0 || a->kv_rows > INT32_MAX) return DSA_ERR_BAD_SHAPE;
     if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
     if (a->kv_format != DSA_KV_BF16 && a->kv_format != DSA_KV_FP8_656) return DSA_ERR_BAD_FORMAT;
+    if (row_stride_bytes(a->kv_format, a->kv_stride_row) < 0) return DSA_ERR_BAD_STRIDE;
     if (a->topk > MAX_CHUNK) return DSA_ERR_UNSUPPORTED;
     if (a->N == 0) return DSA_OK;
     if (!a->q || !a->out || (a->topk > 0 && (!a->kv || !a->indices))) return DSA_ERR_NULL_POINTER;
@@ -1630,6 +1671,7 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* a, void* ws, size_t ws_bytes, vo
     fp.q_sb = a->q_stride_n; fp.q_st = 0; fp.q_sh = a->q_stride_h;
     fp.kv = (const unsigned char*)a->kv;
     fp.kv_total_rows = a->kv_rows;
+    fp.row_bytes = row_stride_bytes(a->kv_format, a->kv_stride_row);
     fp.kv_batch_stride = 0;
     fp.block_table = nullptr;
     fp.block_size = 1;
@@ -1651,6 +1693,9 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* a, void* ws, size_t ws_bytes, vo
 int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* a, void* stream) {
     if (!a) return DSA_ERR_NULL_POINTER;
     if (a->N < 0 || a->total_pages < 0 || a->total_tokens < 0 || a->max_rows < 0) return DSA_ERR_BAD_SHAPE;
+    // row ids carry their pool in bit 30 (dsa_rows.h): each pool stays below 2^30 rows
+    if (a->total_pages >= dsa_rows::MAX_POOL_ROWS || a->total_tokens >= dsa_rows::MAX_POOL_ROWS)
+        return DSA_ERR_BAD_SHAPE;
     if (a->H != HEADS || a->D != DSA_MLA_D_V4 || a->max_rows > MAX_CHUNK) return DSA_ERR_UNSUPPORTED;
     if (a->N == 0) return DSA_OK;
     if (!a->q || !a->out || !a->kv_indptr_prefix || !a->kv_indices_prefix || !a->kv_indptr_extend ||
@@ -1685,6 +1730,8 @@ int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* a, void* stream) {
 int dsa_mla_prefill_v4_fp8(const dsa_mla_prefill_v4_fp8_args* a, void* stream) {
     if (!a) return DSA_ERR_NULL_POINTER;
     if (a->N < 0 || a->total_pages < 0 || a->total_tokens < 0 || a->max_rows < 0) return DSA_ERR_BAD_SHAPE;
+    if (a->total_pages >= dsa_rows::MAX_POOL_ROWS || a->total_tokens >= dsa_rows::MAX_POOL_ROWS)
+        return DSA_ERR_BAD_SHAPE;
     if (a->H != HEADS || a->max_rows > MAX_CHUNK) return DSA_ERR_UNSUPPORTED;
     if (a->N == 0) return DSA_OK;
     if (!a->q_nope || !a->q_rope || !a->out || !a->kv_indptr_prefix || !a->kv_indices_prefix ||

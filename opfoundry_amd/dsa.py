@@ -28,14 +28,26 @@ def _stream(stream) -> Optional[int]:
     return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
 
 
-def kv_format_of(kv: torch.Tensor) -> Tuple[int, int]:
-    """(kv_format, total_rows) of a cache tensor: bf16 [..., 576] or uint8 [..., 656]."""
+def kv_format_of(kv: torch.Tensor) -> Tuple[int, int, int]:
+    """(kv_format, total_rows, row_stride) of a cache tensor: bf16 [..., 576] or uint8
+    [..., 656] with a dense last dim.  Rows may be padded (a view of wider rows): row_stride
+    is the element distance between rows, 0 when they are dense."""
     if kv.dtype == torch.bfloat16 and kv.shape[-1] == abi.D_QK:
-        return abi.KV_BF16, kv.numel() // abi.D_QK
-    if kv.dtype == torch.uint8 and kv.shape[-1] == abi.FP8_ROW_BYTES:
-        return abi.KV_FP8_656, kv.numel() // abi.FP8_ROW_BYTES
-    raise ValueError(f"kv cache must be bf16 [..., 576] or uint8 [..., 656], got {kv.dtype} "
-                     f"{tuple(kv.shape)}")
+        fmt, width = abi.KV_BF16, abi.D_QK
+    elif kv.dtype == torch.uint8 and kv.shape[-1] == abi.FP8_ROW_BYTES:
+        fmt, width = abi.KV_FP8_656, abi.FP8_ROW_BYTES
+    else:
+        raise ValueError(f"kv cache must be bf16 [..., 576] or uint8 [..., 656], got {kv.dtype} "
+                         f"{tuple(kv.shape)}")
+    if kv.stride(-1) != 1:
+        raise ValueError("kv cache rows must have a dense last dim")
+    rs = kv.stride(-2) if kv.dim() >= 2 else width
+    expect = rs
+    for d in range(kv.dim() - 2, -1, -1):
+        if kv.shape[d] > 1 and kv.stride(d) != expect:
+            raise ValueError("kv cache rows must be one uniform stride apart")
+        expect *= kv.shape[d]
+    return fmt, kv.numel() // width, (0 if rs == width else rs)
 
 
 def _need(t: torch.Tensor, dtype, name: str):
@@ -52,7 +64,7 @@ def make_decode_args(q, kv_cache, indices, sm_scale, out, lse, *, seq_lens, bloc
         raise ValueError("q must be [B, s_q, H, 576] with a dense last dim")
     if tuple(indices.shape[:2]) != (B, s_q) or indices.stride(2) != 1:
         raise ValueError("indices must be [B, s_q, topk] with a dense last dim")
-    fmt, rows = kv_format_of(kv_cache)
+    fmt, rows, row_stride = kv_format_of(kv_cache)
     if block_table is not None:
         if block_size is None:
             block_size = kv_cache.shape[-2] if kv_cache.dim() >= 3 else None
@@ -70,6 +82,7 @@ def make_decode_args(q, kv_cache, indices, sm_scale, out, lse, *, seq_lens, bloc
     a.kv_format = fmt
     a.block_size = int(block_size)
     a.kv_batch_stride = int(kv_batch_stride)
+    a.kv_stride_row = row_stride
     a.block_table = _ptr(block_table)
     a.block_table_stride = bt_stride
     a.seq_lens = _ptr(seq_lens)
@@ -141,7 +154,7 @@ def make_decode_csr_args(q, kv, kv_indptr, kv_indices, sm_scale, out, lse, *, s_
         raise ValueError("q must be [B*s_q, H, 576] with a dense last dim")
     if total_q % s_q:
         raise ValueError("q rows must be B * s_q")
-    fmt, rows = kv_format_of(kv)
+    fmt, rows, row_stride = kv_format_of(kv)
     B = kv_indptr.numel() - 1
     if B * s_q != total_q:
         raise ValueError("kv_indptr must have B + 1 entries with B * s_q == q.shape[0]")
@@ -153,6 +166,7 @@ def make_decode_csr_args(q, kv, kv_indptr, kv_indices, sm_scale, out, lse, *, s_
     a.B, a.s_q, a.H, a.total_tokens = B, s_q, H, rows
     a.stride_q_b, a.stride_q_h = q.stride(0), q.stride(1)
     a.stride_o_b, a.stride_o_h = out.stride(0), out.stride(1)
+    a.stride_kv_page = row_stride
     a.kv_format = fmt
     a.max_kv_len = int(max_kv_len)
     a.num_splits = int(num_splits)
@@ -286,12 +300,13 @@ def make_prefill_args(q, kv, indices, sm_scale, out, lse, *, causal=False, causa
         raise ValueError("q must be [N, H, 576] with a dense last dim")
     if indices.shape[0] != N or indices.stride(1) != 1:
         raise ValueError("indices must be [N, topk] with a dense last dim")
-    fmt, rows = kv_format_of(kv)
+    fmt, rows, row_stride = kv_format_of(kv)
     a = PrefillArgs()
     a.q = _ptr(q)
     a.q_stride_n, a.q_stride_h = q.stride(0), q.stride(1)
     a.kv = _ptr(kv)
     a.kv_rows = rows
+    a.kv_stride_row = row_stride
     a.kv_format = fmt
     a.indices = _ptr(indices)
     a.idx_stride_n = indices.stride(0)

@@ -157,6 +157,9 @@ def _decode_args(q, kv, fmt, indices, seq_lens, block_table, block_size, kv_batc
     a.kv_format = fmt
     a.block_size = block_size
     a.kv_batch_stride = kv_batch_stride
+    # rows wider than the format's row are padded rows (the row stride is the array's width)
+    width = D_QK if fmt == KV_BF16 else 656
+    a.kv_stride_row = 0 if kv.shape[1] == width else kv.shape[1]
     a.block_table = _p(block_table)
     a.block_table_stride = 0 if block_table is None else block_table.shape[1]
     a.seq_lens = _p(seq_lens)
@@ -176,10 +179,9 @@ def _prep(q, kv, indices, seq_lens, block_table):
     q = np.ascontiguousarray(q, dtype=np.uint16)
     kv = np.ascontiguousarray(kv)
     fmt = KV_BF16 if kv.dtype == np.uint16 else KV_FP8_656
-    if fmt == KV_BF16:
-        kv = kv.reshape(-1, D_QK)
-    else:
-        kv = kv.reshape(-1, 656)
+    width = D_QK if fmt == KV_BF16 else 656
+    # [..., width] dense rows, or [rows, stride] padded rows (stride > width)
+    kv = kv.reshape(-1, width) if kv.shape[-1] == width else kv.reshape(-1, kv.shape[-1])
     indices = np.ascontiguousarray(indices, dtype=np.int32)
     seq_lens = np.ascontiguousarray(seq_lens, dtype=np.int32)
     if block_table is not None:

@@ -164,12 +164,19 @@ void oracle_dequant_rows_656(const uint8_t* rows, int64_t n, float* out) {
     for (int64_t r = 0; r < n; ++r) oracle_dequant_row_656(rows + r * 656, out + r * D_QK);
 }
 
-static void load_row(const uint8_t* cache, int fmt, int64_t row, float* out) {
+/* Bytes between cache rows: stride in elements of the row format (bf16
+ * elements, or bytes for 656-B rows), 0 = dense rows (defs.h:129). */
+static int64_t row_stride_bytes(int fmt, int64_t stride) {
+    if (fmt == DSA_KV_BF16) return stride ? 2 * stride : DSA_MLA_BF16_ROW_BYTES;
+    return stride ? stride : DSA_MLA_FP8_ROW_BYTES;
+}
+
+static void load_row(const uint8_t* cache, int fmt, int64_t row_bytes, int64_t row, float* out) {
     if (fmt == DSA_KV_BF16) {
-        const uint16_t* p = (const uint16_t*)(cache + row * DSA_MLA_BF16_ROW_BYTES);
+        const uint16_t* p = (const uint16_t*)(cache + row * row_bytes);
         for (int d = 0; d < D_QK; ++d) out[d] = oracle_bf16_to_f32(p[d]);
     } else {
-        oracle_dequant_row_656(cache + row * DSA_MLA_FP8_ROW_BYTES, out);
+        oracle_dequant_row_656(cache + row * row_bytes, out);
     }
 }
 
@@ -303,7 +310,8 @@ static void decode_task(void* vctx, int64_t i, float* scratch) {
     for (int k = c->k_begin; k < c->k_end; ++k) {
         const int64_t row = resolve(a, b, t, idx[k]);
         if (row < 0) continue;
-        load_row((const uint8_t*)a->kv_cache, a->kv_format, row, kv + (size_t)n * D_QK);
+        load_row((const uint8_t*)a->kv_cache, a->kv_format, row_stride_bytes(a->kv_format, a->kv_stride_row), row,
+                 kv + (size_t)n * D_QK);
         ++n;
     }
     const uint16_t* qb = (const uint16_t*)a->q;
@@ -386,7 +394,8 @@ static void prefill_task(void* vctx, int64_t i, float* scratch) {
         const int32_t j = idx[k];
         if (j < 0 || j >= a->kv_rows) continue;
         if (a->causal && (int64_t)j > i + a->causal_offset) continue;
-        load_row((const uint8_t*)a->kv, a->kv_format, j, kv + (size_t)n * D_QK);
+        load_row((const uint8_t*)a->kv, a->kv_format, row_stride_bytes(a->kv_format, a->kv_stride_row), j,
+                 kv + (size_t)n * D_QK);
         ++n;
     }
     const uint16_t* qb = (const uint16_t*)a->q;

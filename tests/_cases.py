@@ -18,7 +18,7 @@ import oracle
 
 D_QK, D_VO = 576, 512
 SM_SCALE = 1.0 / math.sqrt(192.0)
-O_ATOL = 2e-2          # bf16 O: max-abs error bound (every element)
+O_ATOL = 2e-2          # bf16 O: max-abs error bound (every element; one bf16 step where |O| >= 4, o_bound)
 LSE_RTOL = 1e-3        # LSE: |got - ref| <= LSE_RTOL * (1 + |ref|), see lse_rel
 
 
@@ -147,9 +147,40 @@ def lse_rel(got: np.ndarray, ref: np.ndarray) -> float:
     return float(np.max(np.abs(got[fin] - ref[fin]) / (1.0 + np.abs(ref[fin]))))
 
 
+def bf16_step(x: np.ndarray) -> np.ndarray:
+    """Spacing of bf16 values at |x| (2^(e - 7) for |x| in [2^e, 2^(e+1)))."""
+    ax = np.maximum(np.abs(np.asarray(x, np.float64)), np.finfo(np.float32).tiny)
+    return np.exp2(np.floor(np.log2(ax)) - 7)
+
+
+def o_bound(ref: np.ndarray) -> np.ndarray:
+    """Per-element O bound: 2e-2, or one bf16 step where a step is larger.
+
+    The outputs are bf16, so two of them differ by 0 or by at least one step.  For
+    |O| >= 4 a step is 2^-5 = 0.031 > 2e-2: there the 2e-2 bar would demand the
+    identical bf16 value, and a result that differs from the reference by any rounding
+    error (the fp8 656-B path dequantises to fp16, 2^-11 relative) may round to the
+    neighbouring value.  One step is the bound at those elements; below |O| = 4 the
+    bound is 2e-2.
+    """
+    return np.maximum(O_ATOL, bf16_step(ref))
+
+
 def assert_parity(o_got, lse_got, o_ref, lse_ref, what=""):
+    g = oracle.bf16_to_f32(o_got)
+    r = oracle.bf16_to_f32(o_ref)
     e_o = o_max_abs(o_got, o_ref)
     e_l = lse_rel(lse_got, lse_ref)
-    assert e_o <= O_ATOL, f"{what}: O max-abs error {e_o} > {O_ATOL}"
+    if g.size and not np.isnan(g).any():
+        d = np.abs(g.astype(np.float64) - r)
+        over = d > o_bound(r)
+        assert not over.any(), (f"{what}: O error {float(d[over].max())} above the bound at "
+                                f"{int(over.sum())} elements (2e-2, or one bf16 step where |O| >= 4)")
+        stepped = int((d > O_ATOL).sum())
+        if stepped:
+            print(f"[parity] {what}: {stepped} of {d.size} elements (|O| >= 4) differ by one bf16 step",
+                  flush=True)
+    else:
+        assert e_o <= O_ATOL, f"{what}: O max-abs error {e_o} > {O_ATOL}"
     assert e_l <= LSE_RTOL, f"{what}: LSE error {e_l} > {LSE_RTOL} (relative to 1 + |LSE|)"
     return e_o, e_l

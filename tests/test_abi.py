@@ -146,6 +146,10 @@ def test_workspace_and_split_plan(lib):
     (dict(q=None), -1), (dict(indices=None), -1), (dict(seq_lens=None), -1), (dict(out=None), -1),
     (dict(q_stride_h=577), -7), (dict(o_stride_h=514), -7), (dict(q=0x1008), -7),
     (dict(kv_total_rows=-1), -2),
+    # row stride (elements): shorter than a row, not 16-byte aligned, negative
+    (dict(kv_stride_row=575), -7), (dict(kv_stride_row=580), -7), (dict(kv_stride_row=-576), -7),
+    (dict(kv_format=abi.KV_FP8_656, kv_stride_row=600), -7),
+    (dict(kv_format=abi.KV_FP8_656, kv_stride_row=664), -7),
 ])
 def test_decode_rejects_bad_arguments(lib, kw, code):
     a = _decode_args(**kw)
@@ -187,6 +191,16 @@ def _csr_ws(lib, a):
     return rc, n.value
 
 
+def test_row_strides_accepted(lib):
+    """Padded cache rows: any stride of at least one row in whole 16-byte steps."""
+    for fmt, st in ((abi.KV_BF16, 0), (abi.KV_BF16, 576), (abi.KV_BF16, 584), (abi.KV_BF16, 640),
+                    (abi.KV_FP8_656, 0), (abi.KV_FP8_656, 656), (abi.KV_FP8_656, 672)):
+        assert _ws(lib, _decode_args(kv_format=fmt, kv_stride_row=st))[0] == 0
+        assert _csr_ws(lib, _csr_args(kv_format=fmt, stride_kv_page=st))[0] == 0
+    ok = _v4_args(total_pages=(1 << 30) - 1, total_tokens=(1 << 30) - 1, N=0)
+    assert lib.dsa_mla_prefill_v4(ctypes.byref(ok), None) == 0
+
+
 def test_csr_split_plan():
     lib = abi.load_library()
     # 3000 rows per batch exceed one workgroup's 2048: at least two splits
@@ -203,6 +217,8 @@ def test_csr_split_plan():
     (dict(q=None), -1), (dict(kv=None), -1), (dict(kv_indptr=None), -1), (dict(kv_indices=None), -1),
     (dict(out=None), -1), (dict(stride_q_h=577), -7), (dict(stride_o_b=-512), -7),
     (dict(q=0x1004), -7),
+    (dict(stride_kv_page=500), -7), (dict(stride_kv_page=578), -7), (dict(stride_kv_page=-576), -7),
+    (dict(kv_format=abi.KV_FP8_656, stride_kv_page=660), -7),
 ])
 def test_csr_rejects_bad_arguments(lib, kw, code):
     a = _csr_args(**kw)
@@ -302,6 +318,8 @@ def _v4_args(**kw):
     (dict(kv_indices_extend=None), -1), (dict(unified_kv=None), -1), (dict(kv=None), -1),
     (dict(stride_kv_page=500), -7), (dict(stride_kv_page=516), -7), (dict(stride_qo_h=513), -7),
     (dict(q=0x1008), -7), (dict(out=0x5004), -7),
+    # row ids carry their pool in bit 30: each pool stays below 2^30 rows
+    (dict(total_pages=1 << 30), -2), (dict(total_tokens=1 << 30), -2), (dict(total_pages=2 ** 31 - 1), -2),
 ])
 def test_prefill_v4_rejects_bad_arguments(lib, kw, code):
     assert lib.dsa_mla_prefill_v4(ctypes.byref(_v4_args(**kw)), None) == code
@@ -335,6 +353,7 @@ def _prefill_args(**kw):
     (dict(H=32), -3), (dict(N=-1), -2), (dict(topk=-1), -2), (dict(kv_format=3), -4),
     (dict(q=None), -1), (dict(kv=None), -1), (dict(out=None), -1), (dict(indices=None), -1),
     (dict(q_stride_h=100), -7), (dict(out=0x4002), -7), (dict(kv_rows=-3), -2),
+    (dict(kv_stride_row=570), -7), (dict(kv_stride_row=590), -7),
 ])
 def test_prefill_rejects_bad_arguments(lib, kw, code):
     a = _prefill_args(**kw)
@@ -395,6 +414,7 @@ def _v4fp8_args(**kw):
     (dict(unified_kv_nope=None), -1), (dict(kv_rope=None), -1), (dict(kv_indices_extend=None), -1),
     (dict(stride_q_nope_h=520), -7), (dict(stride_kv_nope_page=496), -7), (dict(stride_kv_rope_page=60), -7),
     (dict(stride_o_h=510), -7), (dict(kv_nope=0x5008), -7),
+    (dict(total_pages=1 << 30), -2), (dict(total_tokens=1 << 30), -2),
 ])
 def test_prefill_v4_fp8_rejects_bad_arguments(lib, kw, code):
     assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(_v4fp8_args(**kw)), None) == code

@@ -123,3 +123,52 @@ def test_csr_matches_topk_entry_bitwise(dev):
     torch.cuda.synchronize()
     assert (bits(out).reshape(o_csr.shape) == o_csr).all()
     assert np.array_equal(lse.cpu().numpy().reshape(l_csr.shape), l_csr)
+
+
+def padded_device_rows(kv: np.ndarray, pad: int, dev) -> torch.Tensor:
+    """kv rows inside a wider cache tensor (pad extra elements per row, NaN-filled), viewed as
+    [rows, width]: the kernel must step rows by the padded stride and never read the pad."""
+    width = kv.shape[1]
+    if kv.dtype == np.uint16:
+        big = np.full((kv.shape[0], width + pad), 0x7FC0, np.uint16)
+        big[:, :width] = kv
+        return t16(big, dev)[:, :width]
+    big = np.full((kv.shape[0], width + pad), 0xFF, np.uint8)
+    big[:, :width] = kv
+    return torch.from_numpy(big).to(dev)[:, :width]
+
+
+@pytest.mark.parametrize("fp8,pad", [(False, 64), (True, 16)])
+def test_csr_padded_rows(dev, fp8, pad):
+    """stride_kv_page, the row stride of the latent KV tensor (defs.h:129,
+    opus_attn/dsa_v32/README.md:99): bf16 rows 640 elements apart, 656-B rows 672 bytes apart,
+    the pad NaN-filled.  Split and unsplit against the oracle on the dense rows."""
+    lens = [900, 2048, 37]
+    print(f"[case] csr padded rows fp8={fp8} pad={pad}", flush=True)
+    q, kv, indptr, indices = csr_case(51 + fp8, lens, 2, 5000, fp8=fp8, bad_rows=10)
+    o_ref, l_ref = oracle_csr(q, kv, indptr, indices, 2)
+    kvt = padded_device_rows(kv, pad, dev)
+    assert kvt.stride(0) == kv.shape[1] + pad
+    for ns in (0, 3):
+        out, lse = dsa.mla_decode_csr(t16(q, dev), kvt, torch.from_numpy(indptr).to(dev),
+                                      torch.from_numpy(indices).to(dev), SM_SCALE, s_q=2, num_splits=ns)
+        torch.cuda.synchronize()
+        e = assert_parity(bits(out), lse.cpu().numpy(), o_ref, l_ref, f"csr padded fp8={fp8} splits={ns}")
+        print(f"[case] splits={ns}: max|dO|={e[0]:.3e} max rel dLSE={e[1]:.3e}", flush=True)
+
+
+@pytest.mark.parametrize("ns", [0, 1])
+def test_csr_list_longer_than_bound_is_nan(dev, ns):
+    """max_kv_len below a list's length: that query's O and LSE are NaN (never a silently
+    truncated attention); the other queries are exact."""
+    lens = [3000, 500]
+    print(f"[case] csr underestimated max_kv_len splits={ns}", flush=True)
+    q, kv, indptr, indices = csr_case(57, lens, 1, 4000)
+    o_ref, l_ref = oracle_csr(q, kv, indptr, indices, 1)
+    out, lse = dsa.mla_decode_csr(t16(q, dev), t16(kv, dev), torch.from_numpy(indptr).to(dev),
+                                  torch.from_numpy(indices).to(dev), SM_SCALE, s_q=1, max_kv_len=1024,
+                                  num_splits=ns)
+    torch.cuda.synchronize()
+    lse = lse.cpu().numpy()
+    assert np.isnan(lse[0]).all() and torch.isnan(out[0].float()).all()
+    assert_parity(bits(out)[1:], lse[1:], o_ref[1:], l_ref[1:], "csr bound: intact query")

@@ -129,3 +129,69 @@ def test_prefill_v4_reference_restart(dev):
     w = 8.0 * np.exp(-8 * scale) / (1 + np.exp(-8 * scale))
     oi = oracle.bf16_to_f32(o)[i0]
     assert np.allclose(oi[:, :256], 8.0 - w, atol=2e-2) and np.allclose(oi[:, 256:511], w, atol=2e-2)
+
+
+def test_prefill_v4_high_prefix_ids_are_skipped(dev):
+    """Prefix ids in [2^30, 2^31) beside a small extend pool.  Bit 30 is the kernel's
+    second-pool tag; a prefix id is checked against total_pages before any tag exists, so
+    these ids are skipped like any other id outside the prefix pool (the oracle skips them
+    too), whether or not their low 30 bits name an extend row."""
+    print("[case] V4 prefill prefix ids >= 2^30", flush=True)
+    q, ukv, xkv, sink, ipp, idp, ipe, ide = v4_inputs(45, N=40, total_pages=2048, topk=300, window=16)
+    rng = np.random.default_rng(46)
+    pos = rng.choice(idp.size, 200, replace=False)
+    high = np.concatenate([(1 << 30) + rng.integers(0, xkv.shape[0], 100),   # low bits: an extend row
+                           rng.integers(1 << 30, 2 ** 31, 100)])             # anywhere up to 2^31 - 1
+    idp[pos] = high.astype(np.int32)
+    scale = 1.0 / np.sqrt(D)
+    o_ref, l_ref = oracle.mla_prefill_v4(q, ukv, xkv, sink, ipp, idp, ipe, ide, scale)
+    ts = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    out, lse = dsa.mla_prefill_v4(t16(q, dev), t16(ukv, dev), t16(xkv, dev), ts(sink), ts(ipp), ts(idp),
+                                  ts(ipe), ts(ide), scale)
+    torch.cuda.synchronize()
+    e = assert_parity(bits(out), lse.cpu().numpy(), o_ref, l_ref, "V4 prefill high prefix ids")
+    print(f"[case] max|dO|={e[0]:.3e} max rel dLSE={e[1]:.3e}", flush=True)
+
+
+def test_prefill_v4_extreme_sink(dev):
+    """Sinks far above every score (+200, +60 natural-log units), far below (-200) and near
+    the scores: the maximum is taken over the scores and the sink together
+    (mla_v4_host.cc:469), so O stays finite (about 0 under a dominant sink) and LSE is about
+    the sink.  Lists of one tile (the normalised-P fold) and of many."""
+    print("[case] V4 prefill extreme sink", flush=True)
+    q, ukv, xkv, sink, ipp, idp, ipe, ide = v4_inputs(48, N=48, total_pages=4096, topk=400, window=8)
+    sink = sink.copy()
+    sink[:32], sink[32:64], sink[64:96] = 200.0, -200.0, 60.0
+    sink[96:128] = np.linspace(-3.0, 6.0, 32)
+    scale = 1.0 / np.sqrt(D)
+    o_ref, l_ref = oracle.mla_prefill_v4(q, ukv, xkv, sink, ipp, idp, ipe, ide, scale)
+    ts = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    out, lse = dsa.mla_prefill_v4(t16(q, dev), t16(ukv, dev), t16(xkv, dev), ts(sink), ts(ipp), ts(idp),
+                                  ts(ipe), ts(ide), scale)
+    torch.cuda.synchronize()
+    l = lse.cpu().numpy()
+    assert np.isfinite(oracle.bf16_to_f32(bits(out))).all()
+    e = assert_parity(bits(out), l, o_ref, l_ref, "V4 prefill extreme sink")
+    print(f"[case] max|dO|={e[0]:.3e} max rel dLSE={e[1]:.3e}", flush=True)
+    nonempty = [i for i in range(q.shape[0]) if ipp[i + 1] > ipp[i] or ipe[i + 1] > ipe[i]]
+    assert np.allclose(l[nonempty, :32], 200.0, rtol=1e-6)
+
+
+def test_prefill_v4_rows_beyond_max_rows_are_nan(dev):
+    """max_rows below a query's prefix + extend entries: that query's O and LSE are NaN;
+    queries within the bound are exact."""
+    print("[case] V4 prefill underestimated max_rows", flush=True)
+    q, ukv, xkv, sink, ipp, idp, ipe, ide = v4_inputs(49, N=16, total_pages=2048, topk=300, window=40)
+    n_rows = (ipp[1:] - ipp[:-1]) + (ipe[1:] - ipe[:-1])
+    bound = 305
+    scale = 1.0 / np.sqrt(D)
+    o_ref, l_ref = oracle.mla_prefill_v4(q, ukv, xkv, sink, ipp, idp, ipe, ide, scale)
+    ts = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    out, lse = dsa.mla_prefill_v4(t16(q, dev), t16(ukv, dev), t16(xkv, dev), ts(sink), ts(ipp), ts(idp),
+                                  ts(ipe), ts(ide), scale, max_rows=bound)
+    torch.cuda.synchronize()
+    l = lse.cpu().numpy()
+    over = n_rows > bound
+    assert over.any() and (~over).any()
+    assert np.isnan(l[over]).all() and torch.isnan(out[torch.from_numpy(over).to(dev)].float()).all()
+    assert_parity(bits(out)[~over], l[~over], o_ref[~over], l_ref[~over], "V4 prefill within bound")

@@ -161,3 +161,34 @@ def test_prefill_v4_fp8_reference_restart(dev):
     w = 8.0 * np.exp(-8 * scale) / (1 + np.exp(-8 * scale))
     oi = oracle.bf16_to_f32(o)[i0]
     assert np.allclose(oi[:, :256], 8.0 - w, atol=2e-2) and np.allclose(oi[:, 256:511], w, atol=2e-2)
+
+
+def test_prefill_v4_fp8_high_prefix_ids_are_skipped(dev):
+    """As the bf16 V4 case: prefix ids in [2^30, 2^31) next to a small extend pool are outside
+    the prefix pool and skipped; the oracle skips them too."""
+    print("[case] V4 fp8 prefill prefix ids >= 2^30", flush=True)
+    q, ukv, xkv, sink, lists = v4fp8_inputs(65, N=32, total_pages=1024, topk=200, window=16)
+    rng = np.random.default_rng(66)
+    idp = lists[1]
+    pos = rng.choice(idp.size, 150, replace=False)
+    idp[pos] = np.concatenate([(1 << 30) + rng.integers(0, xkv[0].shape[0], 75),
+                               rng.integers(1 << 30, 2 ** 31, 75)]).astype(np.int32)
+    scale = 1.0 / np.sqrt(512)
+    o_ref, l_ref = oracle.mla_prefill_v4_fp8(*q, *ukv, *xkv, sink, *lists, scale)
+    o, l = run(*to_dev(q, ukv, xkv, dev), sink, lists, scale, dev)
+    e = assert_parity(o, l, o_ref, l_ref, "V4 fp8 prefill high prefix ids")
+    print(f"[case] max|dO|={e[0]:.3e} max rel dLSE={e[1]:.3e}", flush=True)
+
+
+def test_prefill_v4_fp8_extreme_sink(dev):
+    """Sinks far above and far below every score, on fp8 rows: finite O, LSE about the sink."""
+    print("[case] V4 fp8 prefill extreme sink", flush=True)
+    q, ukv, xkv, sink, lists = v4fp8_inputs(67, N=32, total_pages=2048, topk=300, window=8)
+    sink = sink.copy()
+    sink[:64], sink[64:96] = 150.0, -150.0
+    scale = 1.0 / np.sqrt(512)
+    o_ref, l_ref = oracle.mla_prefill_v4_fp8(*q, *ukv, *xkv, sink, *lists, scale)
+    o, l = run(*to_dev(q, ukv, xkv, dev), sink, lists, scale, dev)
+    assert np.isfinite(oracle.bf16_to_f32(o)).all()
+    e = assert_parity(o, l, o_ref, l_ref, "V4 fp8 prefill extreme sink")
+    print(f"[case] max|dO|={e[0]:.3e} max rel dLSE={e[1]:.3e}", flush=True)
