@@ -35,7 +35,8 @@
  * workspace included); strides are in elements; `stream` is a hipStream_t
  * (NULL = the null stream).  Every entry point validates its arguments
  * before any launch and returns 0 on success or a negative DSA_ERR_* code;
- * nothing calls exit().  The library holds no mutable global state, so calls
+ * nothing calls exit().  Apart from the device scratch of
+ * dsa_mla_decode_noalloc the library holds no mutable global state, so calls
  * on distinct streams with distinct workspaces may run concurrently.
  */
 #ifndef DSA_MLA_H_
@@ -77,7 +78,8 @@ enum {
     DSA_ERR_WORKSPACE = -5,
     DSA_ERR_BAD_SPLITS = -6,
     DSA_ERR_BAD_STRIDE = -7,
-    DSA_ERR_HIP = -8
+    DSA_ERR_HIP = -8,
+    DSA_ERR_SCRATCH_LIMIT = -9
 };
 
 /*
@@ -145,6 +147,21 @@ int dsa_mla_decode_num_splits(const dsa_mla_decode_args* args, int32_t* num_spli
  */
 int dsa_mla_decode(const dsa_mla_decode_args* args, void* workspace, size_t workspace_bytes,
                    void* stream);
+
+/*
+ * dsa_mla_decode without a workspace and without any allocation: for callers
+ * that cannot call hipMalloc (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation).  No counterpart in the reference.
+ * The split partials go to a device scratch array the library holds on each
+ * GPU for the life of the process (DSA_MLA_NOALLOC_SCRATCH_BYTES; its address
+ * is looked up on a device's first call).  A call whose partials need more
+ * (dsa_mla_decode_workspace_size) returns DSA_ERR_SCRATCH_LIMIT before any
+ * launch; unsplit calls need none.  Calls that overlap on one GPU share its
+ * scratch and race: serialise them (one stream, or events).  Results equal
+ * dsa_mla_decode's on the same arguments.
+ */
+#define DSA_MLA_NOALLOC_SCRATCH_BYTES (16u << 20)
+int dsa_mla_decode_noalloc(const dsa_mla_decode_args* args, void* stream);
 
 /*
  * Merge split partials: partial_o fp32 [num_splits, rows, H, 512] (each split

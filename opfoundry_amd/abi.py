@@ -34,13 +34,16 @@ ERRORS = {
     -6: "DSA_ERR_BAD_SPLITS",
     -7: "DSA_ERR_BAD_STRIDE",
     -8: "DSA_ERR_HIP",
+    -9: "DSA_ERR_SCRATCH_LIMIT",
 }
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 # Every symbol include/*.h declares (dsa_mla.h, then dsa_topk.h), in declaration order.
 EXPORTED_SYMBOLS = (
     "dsa_mla_decode_workspace_size",
     "dsa_mla_decode_num_splits",
     "dsa_mla_decode",
+    "dsa_mla_decode_noalloc",
     "dsa_mla_decode_csr_workspace_size",
     "dsa_mla_decode_csr",
     "dsa_mla_decode_mxfp8_workspace_size",
@@ -183,6 +186,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.dsa_mla_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeArgs), sz]
     lib.dsa_mla_decode_num_splits.argtypes = [ctypes.POINTER(DecodeArgs), ctypes.POINTER(_i32)]
     lib.dsa_mla_decode.argtypes = [ctypes.POINTER(DecodeArgs), _vp, ctypes.c_size_t, _vp]
+    lib.dsa_mla_decode_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     lib.dsa_mla_decode_csr_workspace_size.argtypes = [ctypes.POINTER(CsrArgs), sz]
     lib.dsa_mla_decode_csr.argtypes = [ctypes.POINTER(CsrArgs), _vp, ctypes.c_size_t, _vp]
     lib.dsa_mla_decode_mxfp8_workspace_size.argtypes = [ctypes.POINTER(MxArgs), sz]

@@ -31,6 +31,7 @@
 #include <stdint.h>
 #include <float.h>
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "../../include/dsa_mla.h"
@@ -1322,6 +1323,36 @@ dsa_kv_quantize_kernel(const __bf16* __restrict__ src, int64_t src_stride, int64
 
 // ------------------------------------------------------------------- host
 
+int decode_launch(const dsa_mla_decode_args* a, int ns, int chunk, void* ws, hipStream_t st);
+
+// Device scratch of dsa_mla_decode_noalloc: the split partials (fp32 O and
+// LSE) of a call live here instead of in a caller workspace.  Every GPU the
+// library runs on holds its own copy for the life of the process.  The name is
+// only a host-side handle: host code uses the per-device address that
+// hipGetSymbolAddress returns, never the array's name.  Nothing in it must
+// start at zero (every split writes all its partials before the combine reads
+// them); calls that overlap on one GPU share it and race.
+static __device__ __align__(256) unsigned char scratch[DSA_MLA_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+void* g_scratch_ptr[MAX_DEVICES];
+std::mutex g_scratch_mu;
+
+// The current device's address of `scratch`, looked up once per device (with
+// that device current, which it is: it is the current device).
+int device_scratch(void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return DSA_ERR_HIP;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return DSA_ERR_HIP;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return DSA_OK;
+}
+
 bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
 // Bytes between cache rows for a row stride given in elements of the row
@@ -1480,6 +1511,9 @@ const char* dsa_mla_strerror(int code) {
     case DSA_ERR_BAD_SPLITS: return "num_splits out of range or too small for top-k";
     case DSA_ERR_BAD_STRIDE: return "misaligned pointer or stride";
     case DSA_ERR_HIP: return "HIP runtime error";
+    case DSA_ERR_SCRATCH_LIMIT:
+        return "the call's split partials exceed the no-allocation entry's device scratch "
+               "(DSA_MLA_NOALLOC_SCRATCH_BYTES); call dsa_mla_decode with a workspace";
     default: return "unknown error";
     }
 }
@@ -1509,7 +1543,29 @@ int dsa_mla_decode(const dsa_mla_decode_args* a, void* ws, size_t ws_bytes, void
     const size_t need = decode_ws_bytes(a, ns);
     if (need && (!ws || ws_bytes < need || ((uintptr_t)ws & 15))) return DSA_ERR_WORKSPACE;
     if (a->B == 0) return DSA_OK;
-    hipStream_t st = (hipStream_t)stream;
+    return decode_launch(a, ns, chunk, ws, (hipStream_t)stream);
+}
+
+int dsa_mla_decode_noalloc(const dsa_mla_decode_args* a, void* stream) {
+    int ns, chunk;
+    const int rc = validate_decode(a, &ns, &chunk);
+    if (rc) return rc;
+    const size_t need = decode_ws_bytes(a, ns);
+    if (need > DSA_MLA_NOALLOC_SCRATCH_BYTES) return DSA_ERR_SCRATCH_LIMIT;
+    if (a->B == 0) return DSA_OK;
+    void* ws = nullptr;
+    if (need) {
+        const int rs = device_scratch(&ws);
+        if (rs) return rs;
+    }
+    return decode_launch(a, ns, chunk, ws, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int decode_launch(const dsa_mla_decode_args* a, int ns, int chunk, void* ws, hipStream_t st) {
     FwdParams fp{};
     fp.q = (const __bf16*)a->q;
     fp.q_sb = a->q_stride_b; fp.q_st = a->q_stride_t; fp.q_sh = a->q_stride_h;
@@ -1542,6 +1598,10 @@ int dsa_mla_decode(const dsa_mla_decode_args* a, void* ws, size_t ws_bytes, void
     return launch_combine(fp.part_o, fp.part_lse, ns, a->B * a->s_q, HEADS, a->s_q, a->out, a->o_stride_b,
                           a->o_stride_t, a->o_stride_h, a->lse, st);
 }
+
+}  // namespace
+
+extern "C" {
 
 int dsa_mla_decode_csr_workspace_size(const dsa_mla_decode_csr_args* a, size_t* bytes) {
     if (!bytes) return DSA_ERR_NULL_POINTER;

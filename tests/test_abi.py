@@ -164,6 +164,22 @@ def test_decode_rejects_missing_workspace(lib):
     assert lib.dsa_mla_decode(ctypes.byref(a), ctypes.c_void_p(0x10008), 1 << 30, None) == -5
 
 
+@pytest.mark.parametrize("kw,code", [
+    (dict(H=64), -3), (dict(B=-1), -2), (dict(q=None), -1), (dict(kv_stride_row=575), -7),
+    (dict(topk=4096, num_splits=1), -6),
+    # 64 splits of 2 x 128 rows: 33.6 MB of partials, beyond the 16 MiB scratch
+    (dict(B=2, num_splits=64), -9),
+])
+def test_decode_noalloc_rejects_before_launch(lib, kw, code):
+    a = _decode_args(**kw)
+    assert lib.dsa_mla_decode_noalloc(ctypes.byref(a), None) == code
+    assert b"scratch" in lib.dsa_mla_strerror(-9)
+
+
+def test_decode_noalloc_empty_batch_is_a_no_op(lib):
+    assert lib.dsa_mla_decode_noalloc(ctypes.byref(_decode_args(B=0)), None) == 0
+
+
 def test_decode_empty_batch_is_a_no_op(lib):
     a = _decode_args(B=0)
     assert lib.dsa_mla_decode(ctypes.byref(a), None, 0, None) == 0
