@@ -56,6 +56,8 @@ extern "C" {
 #define DSA_MLA_FP8_ROW_BYTES 656
 #define DSA_MLA_BF16_ROW_BYTES 1152
 #define DSA_MLA_MAX_SPLITS 64
+/* longest list an entry takes (top-k, max_kv_len, max_rows): INT32_MAX - 2048 */
+#define DSA_MLA_MAX_LIST 2147481599
 #define DSA_MLA_D_V4 512       /* V4 prefill head dim: K = V = a 512-value row */
 #define DSA_MLA_V4_NOPE 448    /* V4 fp8 rows: fp8 NoPE values (then 64 bf16 RoPE) */
 #define DSA_MLA_V4_NOPE_BYTES 512  /* V4 fp8 NoPE stream row: 448 codes, 14 E8M0, pad */
@@ -95,6 +97,8 @@ enum {
  *           one split the top-k list of every query token is cut into
  *           num_splits contiguous chunks whose partial results (fp32 O and
  *           LSE, kept in the workspace) are merged by the combine kernel.
+ *           A split of any length runs in one workgroup (its list is walked
+ *           2048 entries at a time), so one split is always allowed.
  */
 typedef struct {
     const void* q;
@@ -329,10 +333,10 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* args, void* workspace, size_t wo
  * stride_kv_page elements apart.  A row outside its pool is skipped; a query
  * with no rows gets O = 0 (and LSE = +inf).  lse (an addition to the
  * reference, may be NULL) is the natural log of the denominator, sink
- * included.  max_rows bounds the prefix + extend entries of any query and
- * must be <= 2048 (a query with more gets NaN O and LSE, never a silently
- * truncated attention); H must be 128; total_pages and total_tokens must be
- * below 2^30.
+ * included.  max_rows bounds the prefix + extend entries of any query (a
+ * query with more gets NaN O and LSE, never a silently truncated attention);
+ * a list of any length runs in the query's one workgroup, 2048 entries at a
+ * time.  H must be 128; total_pages and total_tokens must be below 2^30.
  */
 typedef struct {
     const void* q;

@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(PKG_DIR, "_build", "libdsa_mla.so")
 D_QK, D_NOPE, D_ROPE, D_VO = 576, 512, 64, 512
 FP8_ROW_BYTES, BF16_ROW_BYTES = 656, 1152
 MAX_SPLITS = 64
+MAX_LIST = 2 ** 31 - 1 - 2048      # DSA_MLA_MAX_LIST: longest top-k / max_kv_len / max_rows
 
 KV_BF16 = 0
 KV_FP8_656 = 1

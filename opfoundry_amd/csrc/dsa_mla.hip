@@ -47,7 +47,10 @@ constexpr int HEADS = 128;                 // heads per workgroup (4 waves x 32)
 constexpr int NWAVE = 4;
 constexpr int NTHR = NWAVE * 64;
 constexpr int TILE = 32;                   // latent rows per tile
-constexpr int MAX_CHUNK = 2048;            // top-k entries one workgroup can take
+constexpr int MAX_CHUNK = 2048;            // list entries a workgroup resolves at a time
+// longest list (top-k, max_kv_len, max_rows): entry positions stay int32
+constexpr int32_t MAX_LIST = DSA_MLA_MAX_LIST;
+static_assert(MAX_LIST == INT32_MAX - MAX_CHUNK, "list positions + one chunk fit int32");
 constexpr int KS_NOPE = D_NOPE / 16;       // 16-deep k-steps over the NoPE dims (32)
 constexpr int KS_ALL = D_QK / 16;          // all k-steps (36)
 constexpr float LOG2E = 1.4426950408889634f;
@@ -422,67 +425,84 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         truncated = count > k_cap;
         idx = p.kv_indices + kb;
     } else {
-        k1 = min(k0 + p.chunk, p.topk);
+        k1 = (int)min((int64_t)k0 + p.chunk, (int64_t)p.topk);
         const int64_t Lq = p.seq_lens ? (int64_t)p.seq_lens[b] : p.seq_len_default;
         jmax = Lq;
         if (p.causal == 1) jmax = min(Lq, Lq - p.s_q + t + 1);
         else if (p.causal == 2) jmax = min(Lq, (int64_t)b + p.causal_offset + 1);
         idx = p.indices + (int64_t)b * p.idx_sb + (int64_t)t * p.idx_st;
     }
+    // The split's entries are taken MAX_CHUNK at a time (the row list holds
+    // one chunk); the softmax state and the O accumulators carry over from
+    // one chunk to the next, so a list of any length needs no partials.  An
+    // empty range is one empty chunk.
+    const int nchunks = k1 > k0 ? (k1 - k0 + MAX_CHUNK - 1) / MAX_CHUNK : 1;
 
-    constexpr int PER_T = MAX_CHUNK / NTHR;  // 8 entries per thread
-    int32_t rows_local[PER_T];
-    int cnt = 0;
-    {
-        // all loads first (they overlap), then the rules of dsa_rows.h; a V4
-        // entry is checked against the pool its list names (ext[e])
-        int32_t jv[PER_T];
-        bool ext[PER_T];
+    // entries [kc0, min(kc0 + MAX_CHUNK, k1)) -> the compacted row list;
+    // sets n_valid and ntiles (ends with a workgroup barrier)
+    int n_valid = 0, ntiles = 0;
+    bool any_rows = false;
+    auto resolve_chunk = [&](int c) {
+        const int kc0 = k0 + c * MAX_CHUNK;
+        const int kc1 = min(kc0 + MAX_CHUNK, k1);
+        constexpr int PER_T = MAX_CHUNK / NTHR;  // 8 entries per thread
+        int32_t rows_local[PER_T];
+        int cnt = 0;
+        {
+            // all loads first (they overlap), then the rules of dsa_rows.h; a V4
+            // entry is checked against the pool its list names (ext[e])
+            int32_t jv[PER_T];
+            bool ext[PER_T];
 #pragma unroll
-        for (int e = 0; e < PER_T; ++e) {
-            const int k = k0 + tid * PER_T + e;
-            ext[e] = L::D512 && p.ind_pre && k >= v4_np;
-            if (k >= k1) jv[e] = -1;
-            else jv[e] = ext[e] ? p.idx_ext[v4_eb + (k - v4_np)] : idx[k];
+            for (int e = 0; e < PER_T; ++e) {
+                const int k = kc0 + tid * PER_T + e;
+                ext[e] = L::D512 && p.ind_pre && k >= v4_np;
+                if (k >= kc1) jv[e] = -1;
+                else jv[e] = ext[e] ? p.idx_ext[v4_eb + (k - v4_np)] : idx[k];
+            }
+#pragma unroll
+            for (int e = 0; e < PER_T; ++e) {
+                if (L::D512 && p.ind_pre)
+                    rows_local[e] = ext[e] ? dsa_rows::v4_extend_row(jv[e], p.kv2_rows)
+                                           : dsa_rows::v4_prefix_row(jv[e], p.kv_total_rows);
+                else
+                    rows_local[e] = p.kv_indptr ? dsa_rows::csr_row(jv[e], p.kv_total_rows)
+                                                : (int32_t)resolve_row(p, b, jmax, jv[e]);
+                cnt += rows_local[e] >= 0 ? 1 : 0;
+            }
         }
+        int incl = cnt;
 #pragma unroll
-        for (int e = 0; e < PER_T; ++e) {
-            if (L::D512 && p.ind_pre)
-                rows_local[e] = ext[e] ? dsa_rows::v4_extend_row(jv[e], p.kv2_rows)
-                                       : dsa_rows::v4_prefix_row(jv[e], p.kv_total_rows);
-            else
-                rows_local[e] = p.kv_indptr ? dsa_rows::csr_row(jv[e], p.kv_total_rows)
-                                            : (int32_t)resolve_row(p, b, jmax, jv[e]);
-            cnt += rows_local[e] >= 0 ? 1 : 0;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += v;
         }
-    }
-    int incl = cnt;
+        // (the barrier also ends every wave's use of the previous chunk's
+        // row list, tile buffers and P buffers)
+        if (lane == 63) s_misc[wave] = incl;
+        __syncthreads();
+        int wbase = 0, nv = 0;
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int v = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += v;
-    }
-    if (lane == 63) s_misc[wave] = incl;
-    __syncthreads();
-    int wbase = 0, n_valid = 0;
+        for (int w = 0; w < NWAVE; ++w) {
+            const int s = s_misc[w];
+            wbase += w < wave ? s : 0;
+            nv += s;
+        }
+        {
+            int pos = wbase + incl - cnt;
 #pragma unroll
-    for (int w = 0; w < NWAVE; ++w) {
-        const int s = s_misc[w];
-        wbase += w < wave ? s : 0;
-        n_valid += s;
-    }
-    {
-        int pos = wbase + incl - cnt;
-#pragma unroll
-        for (int e = 0; e < PER_T; ++e)
-            if (rows_local[e] >= 0) s_rows[pos++] = rows_local[e];
-    }
-    __syncthreads();
-    const int ntiles = (n_valid + TILE - 1) / TILE;
-    // Pad the last tile with copies of the first valid row: every gathered
-    // row is finite cache data, and the softmax masks the padding rows.
-    if (tid < TILE && n_valid > 0 && n_valid + tid < ntiles * TILE) s_rows[n_valid + tid] = s_rows[0];
-    __syncthreads();
+            for (int e = 0; e < PER_T; ++e)
+                if (rows_local[e] >= 0) s_rows[pos++] = rows_local[e];
+        }
+        n_valid = nv;
+        ntiles = (nv + TILE - 1) / TILE;
+        any_rows = any_rows || nv > 0;
+        __syncthreads();
+        // Pad the last tile with copies of the first valid row: every gathered
+        // row is finite cache data, and the softmax masks the padding rows.
+        if (tid < TILE && nv > 0 && nv + tid < ntiles * TILE) s_rows[nv + tid] = s_rows[0];
+        __syncthreads();
+    };
 
     // bf16 ring slot -> tile buffer
     auto slot_buf = [&](int s) -> lds_ptr { return s == 0 ? T0 : (s == 1 ? T1 : RING); };
@@ -714,30 +734,25 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // dims across the waves, so each gathered V value is read by one wave).
     f32x16 o[D_VO / 32];
     float m_ref = 0.0f, l_lane = 0.0f, s_max = -INFINITY;
-    // Q (and the index loads) complete before the first gathers are issued:
-    // inside the loop the only vector-memory loads are the LDS-DMA gathers,
-    // counted explicitly, and the first tile waits for its own rows alone.
-    wait_vm<0>();
-    if constexpr (L::F16) {
-        // the NoPE part of Q is converted to fp16 for the fp16 MFMAs
+    // Q conversion, once its loads have landed
+    auto convert_q = [&]() {
+        if constexpr (L::F16) {
+            // the NoPE part of Q is converted to fp16 for the fp16 MFMAs
 #pragma unroll
-        for (int ks = 0; ks < KS_NOPE; ++ks)
+            for (int ks = 0; ks < KS_NOPE; ++ks)
 #pragma unroll
-            for (int w = 0; w < 4; ++w) qf[ks][w] = bf16x2_to_f16x2(qf[ks][w]);
-    } else if constexpr (L::MX) {
-        // fp8 NoPE of Q -> bf16: dims 16ks + 8hi .. +7 lie in scale block ks / 2
+                for (int w = 0; w < 4; ++w) qf[ks][w] = bf16x2_to_f16x2(qf[ks][w]);
+        } else if constexpr (L::MX) {
+            // fp8 NoPE of Q -> bf16: dims 16ks + 8hi .. +7 lie in scale block ks / 2
 #pragma unroll
-        for (int ks = 0; ks < L::Q8_KS; ++ks) {
-            const unsigned e = (q_scales[ks >> 3] >> (8 * ((ks >> 1) & 3))) & 0xFFu;
-            qf[ks] = mx_to_bf16(qf[ks][0], qf[ks][1], e);
+            for (int ks = 0; ks < L::Q8_KS; ++ks) {
+                const unsigned e = (q_scales[ks >> 3] >> (8 * ((ks >> 1) & 3))) & 0xFFu;
+                qf[ks] = mx_to_bf16(qf[ks][0], qf[ks][1], e);
+            }
         }
-    }
-    constexpr int NPRE = FP8 ? 3 : 2;       // tiles in flight before the loop
+    };
+    constexpr int NPRE = FP8 ? 3 : 2;       // tiles in flight before a chunk's loop
     GatherRows gnext;
-#pragma unroll
-    for (int s = 0; s < NPRE; ++s)
-        if (s < ntiles) issue_rows(load_rows(s), s);
-    if (NPRE < ntiles) gnext = load_rows(NPRE);
 
     // P values -> MFMA operand (fp16 for the 656-B cache, else bf16)
     auto to_p = [&](const float* e) -> u32x4 {
@@ -859,7 +874,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             first_tile = false;
         }
         mask_rows(sacc, rows_left);
-        if (ntiles == 1 && it == 0) {
+        if (nchunks == 1 && ntiles == 1 && it == 0) {
             // Single-tile list: fold the exact sum into the reference, so
             // that p = exp2(s - m_ref) is already normalised when it is
             // rounded - the order the reference uses
@@ -981,7 +996,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             first_tile = false;
         }
         mask_track(s, 0);
-        if (ntiles == 1) {
+        if (nchunks == 1 && ntiles == 1) {
             float lt = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) lt += __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c_s, -m_ref));
@@ -1042,72 +1057,79 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         l_lane = 0.0f;
         s_max = -INFINITY;
         first_tile = pass == 0;
-        if (pass > 0) {
+        for (int c = 0; c < nchunks; ++c) {
+            // a one-chunk list keeps its row list for the second pass
+            if (pass == 0 || nchunks > 1) resolve_chunk(c);
+            // Q and the index loads complete before the gathers are issued: in
+            // the tile loop the only vector-memory loads are the LDS-DMA gathers,
+            // counted explicitly, and the first tile waits for its own rows alone.
+            wait_vm<0>();
+            if (pass == 0 && c == 0) convert_q();
 #pragma unroll
             for (int s = 0; s < NPRE; ++s)
                 if (s < ntiles) issue_rows(load_rows(s), s);
             if (NPRE < ntiles) gnext = load_rows(NPRE);
-        }
-        if constexpr (FP8) {
-            if (ntiles > 0) {
-                // tile 0 landed (tiles 1, 2 may still be in flight)
-                wait_tiles(min(ntiles, NPRE) - 1);
-                tile_barrier();
-                dequant(RING, T0);
-            }
-            // Two tiles per trip, so that the buffer being read and the one
-            // being filled are distinct LDS objects in each step.
-            for (int it = 0; it < ntiles; it += 2) {
+            if constexpr (FP8) {
+                if (ntiles > 0) {
+                    // tile 0 landed (tiles 1, 2 may still be in flight)
+                    wait_tiles(min(ntiles, NPRE) - 1);
+                    tile_barrier();
+                    dequant(RING, T0);
+                }
+                // Two tiles per trip, so that the buffer being read and the one
+                // being filled are distinct LDS objects in each step.
+                for (int it = 0; it < ntiles; it += 2) {
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int ii = it + h;
-                    if (ii < ntiles) {
-                        // tile ii+1 (dequantised in this step) must have landed
-                        wait_tiles(ii + 2 < ntiles ? 1 : 0);
-                        tile_barrier();
-                        step(ii, h == 0 ? T0 : T1, h == 0 ? T1 : T0);
+                    for (int h = 0; h < 2; ++h) {
+                        const int ii = it + h;
+                        if (ii < ntiles) {
+                            // tile ii+1 (dequantised in this step) must have landed
+                            wait_tiles(ii + 2 < ntiles ? 1 : 0);
+                            tile_barrier();
+                            step(ii, h == 0 ? T0 : T1, h == 0 ? T1 : T0);
+                        }
                     }
                 }
+            } else {
+                // ring slot of tile j: j % 3.  Tiles 0 and 1 were issued above.
+                if (ntiles > 0) {
+                    wait_tiles(ntiles > 1 ? 1 : 0);    // tile 0 landed
+                    tile_barrier();
+                    f32x16 s0 = qk(slot_buf(0), [](int) {});
+                    soft_first(s0, PX);
+                }
+                int slot_cur = 0;        // ring slot of tile `it`
+                // every tile but the last: QK^T of the next tile, PV of this one
+                for (int it = 0; it + 1 < ntiles; ++it) {
+                    const int slot_nxt = slot_cur == 2 ? 0 : slot_cur + 1;
+                    // tile it+1 landed (the only tile in flight); after the barrier
+                    // every wave's P of tile it is visible and every wave is done
+                    // with iteration it-1, whose ring slot receives tile it+2
+                    wait_vm<0>();
+                    tile_barrier();
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (it + NPRE < ntiles) issue_rows(gnext, slot_nxt == 2 ? 0 : slot_nxt + 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    f32x16 sn = qk(slot_buf(slot_nxt), [](int) {});
+                    if (it + NPRE + 1 < ntiles) gnext = load_rows(it + NPRE + 1);
+                    mask_track(sn, it + 1);
+                    float en[16];
+                    pv_pipe(slot_buf(slot_cur), PX + (it & 1) * PXB, sn, en, std::true_type{});
+                    const lds_ptr px_nxt = PX + ((it + 1) & 1) * PXB;
+                    p_half(en, 0, px_nxt);
+                    p_half(en, 1, px_nxt);
+                    slot_cur = slot_nxt;
+                }
+                if (ntiles > 0) {
+                    // the last tile: PV only (its P is published by this barrier)
+                    tile_barrier();
+                    float en[16];
+                    pv_pipe(slot_buf(slot_cur), PX + ((ntiles - 1) & 1) * PXB, f32x16{}, en, std::false_type{});
+                }
             }
-        } else {
-            // ring slot of tile j: j % 3.  Tiles 0 and 1 were issued above.
-            if (ntiles > 0) {
-                wait_tiles(ntiles > 1 ? 1 : 0);    // tile 0 landed
-                tile_barrier();
-                f32x16 s0 = qk(slot_buf(0), [](int) {});
-                soft_first(s0, PX);
-            }
-            int slot_cur = 0;        // ring slot of tile `it`
-            // every tile but the last: QK^T of the next tile, PV of this one
-            for (int it = 0; it + 1 < ntiles; ++it) {
-                const int slot_nxt = slot_cur == 2 ? 0 : slot_cur + 1;
-                // tile it+1 landed (the only tile in flight); after the barrier
-                // every wave's P of tile it is visible and every wave is done
-                // with iteration it-1, whose ring slot receives tile it+2
-                wait_vm<0>();
-                tile_barrier();
-                __builtin_amdgcn_sched_barrier(0);
-                if (it + NPRE < ntiles) issue_rows(gnext, slot_nxt == 2 ? 0 : slot_nxt + 1);
-                __builtin_amdgcn_sched_barrier(0);
-                f32x16 sn = qk(slot_buf(slot_nxt), [](int) {});
-                if (it + NPRE + 1 < ntiles) gnext = load_rows(it + NPRE + 1);
-                mask_track(sn, it + 1);
-                float en[16];
-                pv_pipe(slot_buf(slot_cur), PX + (it & 1) * PXB, sn, en, std::true_type{});
-                const lds_ptr px_nxt = PX + ((it + 1) & 1) * PXB;
-                p_half(en, 0, px_nxt);
-                p_half(en, 1, px_nxt);
-                slot_cur = slot_nxt;
-            }
-            if (ntiles > 0) {
-                // the last tile: PV only (its P is published by this barrier)
-                tile_barrier();
-                float en[16];
-                pv_pipe(slot_buf(slot_cur), PX + ((ntiles - 1) & 1) * PXB, f32x16{}, en, std::false_type{});
-            }
+            // drain in-flight gathers before the ring can be reused or left
+            wait_vm<0>();
         }
-        // drain in-flight gathers before the ring can be reused or left
-        wait_vm<0>();
         o_fence(o);
         // per head: the largest score of the pass (log2 units); NaN compares false
         const float top = fmaxf(s_max, __shfl_xor(s_max, 32, 64)) * c_s;
@@ -1125,7 +1147,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // and references are per head, owned by the head's QK wave: exchange them.
     const float l_rows = l_lane + __shfl_xor(l_lane, 32, 64);
     // rows were attended (their P may all have underflowed under a dominant sink)
-    const bool has = n_valid > 0;
+    const bool has = any_rows;
     // the softmax denominator: the rows' sum plus an attention sink
     // (mla_v4_host.cc:469-472; LSE then covers the sink as well)
     float l = l_rows, m_fin = m_ref, o_scale = 1.0f;
@@ -1139,7 +1161,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // one tile: P is normalised.  A list longer than the caller's bound
     // (max_kv_len / max_rows) was cut: its outputs are NaN, never a silently
     // truncated attention.
-    if (hi == 0) s_l[head] = truncated ? __builtin_nanf("") : (has ? (ntiles == 1 ? 1.0f : o_scale / l) : 0.0f);
+    if (hi == 0) s_l[head] = truncated ? __builtin_nanf("") : (has ? (nchunks == 1 && ntiles == 1 ? 1.0f : o_scale / l) : 0.0f);
     if (hi == 0) {
         const float lse_v = truncated ? __builtin_nanf("") : (m_fin + __builtin_amdgcn_logf(l)) * LN2;
         if (p.part_o == nullptr) {
@@ -1369,19 +1391,17 @@ int ilog2(int v) { int s = 0; while ((1 << s) < v) ++s; return s; }
 
 int auto_splits(int64_t queries, int topk) {
     int ns = 1;
-    const int min_split = (topk + MAX_CHUNK - 1) / MAX_CHUNK;
     if (queries > 0 && queries < 256) {
         const int64_t want = (256 + queries - 1) / queries;
         const int64_t by_len = (topk + 255) / 256;  // keep >= 8 tiles per split
         ns = (int)std::min<int64_t>(want, std::max<int64_t>(1, by_len));
     }
-    ns = std::max(ns, min_split);
     return std::min(ns, DSA_MLA_MAX_SPLITS);
 }
 
 int validate_decode(const dsa_mla_decode_args* a, int* ns_out, int* chunk_out) {
     if (!a) return DSA_ERR_NULL_POINTER;
-    if (a->B < 0 || a->s_q <= 0 || a->topk < 0) return DSA_ERR_BAD_SHAPE;
+    if (a->B < 0 || a->s_q <= 0 || a->topk < 0 || a->topk > MAX_LIST) return DSA_ERR_BAD_SHAPE;
     if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
     if (a->kv_format != DSA_KV_BF16 && a->kv_format != DSA_KV_FP8_656) return DSA_ERR_BAD_FORMAT;
     if (a->kv_total_rows < 0 || a->kv_total_rows > INT32_MAX) return DSA_ERR_BAD_SHAPE;
@@ -1390,7 +1410,6 @@ int validate_decode(const dsa_mla_decode_args* a, int* ns_out, int* chunk_out) {
     if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
     const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q, a->topk);
     const int chunk = a->topk == 0 ? 0 : (a->topk + ns - 1) / ns;
-    if (chunk > MAX_CHUNK) return a->num_splits ? DSA_ERR_BAD_SPLITS : DSA_ERR_UNSUPPORTED;
     if (a->B > 0 && a->topk > 0) {
         if (!a->q || !a->kv_cache || !a->seq_lens || !a->indices || !a->out) return DSA_ERR_NULL_POINTER;
         if ((a->q_stride_h % 8) != 0 || (a->q_stride_t % 8) != 0 || (a->q_stride_b % 8) != 0)
@@ -1434,14 +1453,14 @@ int launch_combine(const float* po, const float* pl, int ns, int rows, int H, in
 
 int validate_csr(const dsa_mla_decode_csr_args* a, int* ns_out, int* chunk_out) {
     if (!a) return DSA_ERR_NULL_POINTER;
-    if (a->B < 0 || a->s_q <= 0 || a->max_kv_len < 0 || a->total_tokens < 0) return DSA_ERR_BAD_SHAPE;
+    if (a->B < 0 || a->s_q <= 0 || a->max_kv_len < 0 || a->max_kv_len > MAX_LIST || a->total_tokens < 0)
+        return DSA_ERR_BAD_SHAPE;
     if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
     if (a->kv_format != DSA_KV_BF16 && a->kv_format != DSA_KV_FP8_656) return DSA_ERR_BAD_FORMAT;
     if (row_stride_bytes(a->kv_format, a->stride_kv_page) < 0) return DSA_ERR_BAD_STRIDE;
     if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
     const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q, a->max_kv_len);
     const int chunk = a->max_kv_len == 0 ? 0 : (a->max_kv_len + ns - 1) / ns;
-    if (chunk > MAX_CHUNK) return a->num_splits ? DSA_ERR_BAD_SPLITS : DSA_ERR_UNSUPPORTED;
     if (a->B > 0) {
         // the kernel reads Q even when every list is empty
         if (!a->out || !a->kv_indptr || !a->q) return DSA_ERR_NULL_POINTER;
@@ -1463,12 +1482,12 @@ size_t csr_ws_bytes(const dsa_mla_decode_csr_args* a, int ns) {
 
 int validate_mx(const dsa_mla_decode_mxfp8_args* a, int* ns_out, int* chunk_out) {
     if (!a) return DSA_ERR_NULL_POINTER;
-    if (a->B < 0 || a->s_q <= 0 || a->max_kv_len < 0 || a->total_tokens < 0) return DSA_ERR_BAD_SHAPE;
+    if (a->B < 0 || a->s_q <= 0 || a->max_kv_len < 0 || a->max_kv_len > MAX_LIST || a->total_tokens < 0)
+        return DSA_ERR_BAD_SHAPE;
     if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
     if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
     const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q, a->max_kv_len);
     const int chunk = a->max_kv_len == 0 ? 0 : (a->max_kv_len + ns - 1) / ns;
-    if (chunk > MAX_CHUNK) return a->num_splits ? DSA_ERR_BAD_SPLITS : DSA_ERR_UNSUPPORTED;
     if (a->B > 0) {
         // the kernel reads Q even when every list is empty
         if (!a->out || !a->kv_indptr || !a->q_nope || !a->q_scale || !a->q_rope) return DSA_ERR_NULL_POINTER;
@@ -1708,7 +1727,7 @@ int dsa_mla_prefill_workspace_size(const dsa_mla_prefill_args* a, size_t* bytes)
     if (!a || !bytes) return DSA_ERR_NULL_POINTER;
     if (a->N < 0 || a->topk < 0 || a->kv_rows < 0) return DSA_ERR_BAD_SHAPE;
     if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
-    if (a->topk > MAX_CHUNK) return DSA_ERR_UNSUPPORTED;
+    if (a->topk > MAX_LIST) return DSA_ERR_BAD_SHAPE;
     *bytes = 0;
     return DSA_OK;
 }
@@ -1720,7 +1739,7 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* a, void* ws, size_t ws_bytes, vo
     if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
     if (a->kv_format != DSA_KV_BF16 && a->kv_format != DSA_KV_FP8_656) return DSA_ERR_BAD_FORMAT;
     if (row_stride_bytes(a->kv_format, a->kv_stride_row) < 0) return DSA_ERR_BAD_STRIDE;
-    if (a->topk > MAX_CHUNK) return DSA_ERR_UNSUPPORTED;
+    if (a->topk > MAX_LIST) return DSA_ERR_BAD_SHAPE;
     if (a->N == 0) return DSA_OK;
     if (!a->q || !a->out || (a->topk > 0 && (!a->kv || !a->indices))) return DSA_ERR_NULL_POINTER;
     if ((a->q_stride_n % 8) || (a->q_stride_h % 8) || (a->o_stride_n % 4) || (a->o_stride_h % 4))
@@ -1756,7 +1775,8 @@ int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* a, void* stream) {
     // row ids carry their pool in bit 30 (dsa_rows.h): each pool stays below 2^30 rows
     if (a->total_pages >= dsa_rows::MAX_POOL_ROWS || a->total_tokens >= dsa_rows::MAX_POOL_ROWS)
         return DSA_ERR_BAD_SHAPE;
-    if (a->H != HEADS || a->D != DSA_MLA_D_V4 || a->max_rows > MAX_CHUNK) return DSA_ERR_UNSUPPORTED;
+    if (a->max_rows > MAX_LIST) return DSA_ERR_BAD_SHAPE;
+    if (a->H != HEADS || a->D != DSA_MLA_D_V4) return DSA_ERR_UNSUPPORTED;
     if (a->N == 0) return DSA_OK;
     if (!a->q || !a->out || !a->kv_indptr_prefix || !a->kv_indices_prefix || !a->kv_indptr_extend ||
         !a->kv_indices_extend)
@@ -1792,7 +1812,8 @@ int dsa_mla_prefill_v4_fp8(const dsa_mla_prefill_v4_fp8_args* a, void* stream) {
     if (a->N < 0 || a->total_pages < 0 || a->total_tokens < 0 || a->max_rows < 0) return DSA_ERR_BAD_SHAPE;
     if (a->total_pages >= dsa_rows::MAX_POOL_ROWS || a->total_tokens >= dsa_rows::MAX_POOL_ROWS)
         return DSA_ERR_BAD_SHAPE;
-    if (a->H != HEADS || a->max_rows > MAX_CHUNK) return DSA_ERR_UNSUPPORTED;
+    if (a->max_rows > MAX_LIST) return DSA_ERR_BAD_SHAPE;
+    if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
     if (a->N == 0) return DSA_OK;
     if (!a->q_nope || !a->q_rope || !a->out || !a->kv_indptr_prefix || !a->kv_indices_prefix ||
         !a->kv_indptr_extend || !a->kv_indices_extend)

@@ -134,15 +134,17 @@ def test_workspace_and_split_plan(lib):
     assert rc == 0 and ws >= ns_small * 2 * 128 * 513 * 4
     rc, ws1 = _ws(lib, _decode_args(B=2, num_splits=1))
     assert rc == 0 and ws1 == 0
-    # top-k beyond one workgroup's chunk forces a split
+    # enough queries to fill the chip: a long list runs unsplit (the workgroup
+    # walks it 2048 entries at a time)
     rc, ns_big = _splits(lib, _decode_args(B=512, topk=4096))
-    assert rc == 0 and ns_big >= 2
+    assert rc == 0 and ns_big == 1
+    assert _ws(lib, _decode_args(B=512, topk=4096))[1] == 0
 
 
 @pytest.mark.parametrize("kw,code", [
     (dict(H=64), -3), (dict(H=0), -3), (dict(B=-1), -2), (dict(s_q=0), -2), (dict(topk=-5), -2),
     (dict(kv_format=7), -4), (dict(num_splits=65), -6), (dict(num_splits=-1), -6),
-    (dict(topk=4096, num_splits=1), -6), (dict(block_size=0), -2),
+    (dict(topk=2 ** 31 - 1), -2), (dict(block_size=0), -2),
     (dict(q=None), -1), (dict(indices=None), -1), (dict(seq_lens=None), -1), (dict(out=None), -1),
     (dict(q_stride_h=577), -7), (dict(o_stride_h=514), -7), (dict(q=0x1008), -7),
     (dict(kv_total_rows=-1), -2),
@@ -166,7 +168,7 @@ def test_decode_rejects_missing_workspace(lib):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(H=64), -3), (dict(B=-1), -2), (dict(q=None), -1), (dict(kv_stride_row=575), -7),
-    (dict(topk=4096, num_splits=1), -6),
+    (dict(topk=2 ** 31 - 1), -2),
     # 64 splits of 2 x 128 rows: 33.6 MB of partials, beyond the 16 MiB scratch
     (dict(B=2, num_splits=64), -9),
 ])
@@ -219,7 +221,7 @@ def test_row_strides_accepted(lib):
 
 def test_csr_split_plan():
     lib = abi.load_library()
-    # 3000 rows per batch exceed one workgroup's 2048: at least two splits
+    # few queries: the planner splits the lists to fill the chip
     rc, ws = _csr_ws(lib, _csr_args())
     assert rc == 0 and ws >= 2 * 4 * 2 * 128 * 513 * 4
     rc, ws1 = _csr_ws(lib, _csr_args(max_kv_len=2048, B=512, s_q=1))
@@ -229,7 +231,7 @@ def test_csr_split_plan():
 @pytest.mark.parametrize("kw,code", [
     (dict(H=64), -3), (dict(B=-1), -2), (dict(s_q=0), -2), (dict(max_kv_len=-1), -2),
     (dict(total_tokens=-1), -2), (dict(kv_format=9), -4), (dict(num_splits=65), -6),
-    (dict(max_kv_len=4096, num_splits=1), -6), (dict(max_kv_len=200000), -3),
+    (dict(max_kv_len=2 ** 31 - 1), -2),
     (dict(q=None), -1), (dict(kv=None), -1), (dict(kv_indptr=None), -1), (dict(kv_indices=None), -1),
     (dict(out=None), -1), (dict(stride_q_h=577), -7), (dict(stride_o_b=-512), -7),
     (dict(q=0x1004), -7),
@@ -291,7 +293,7 @@ def test_mxfp8_split_plan(lib):
 @pytest.mark.parametrize("kw,code", [
     (dict(H=64), -3), (dict(B=-1), -2), (dict(s_q=0), -2), (dict(max_kv_len=-1), -2),
     (dict(total_tokens=-1), -2), (dict(num_splits=65), -6),
-    (dict(max_kv_len=4096, num_splits=1), -6), (dict(max_kv_len=200000), -3),
+    (dict(max_kv_len=2 ** 31 - 1), -2),
     (dict(q_nope=None), -1), (dict(q_scale=None), -1), (dict(q_rope=None), -1),
     (dict(kv_nope=None), -1), (dict(kv_scale=None), -1), (dict(kv_rope=None), -1),
     (dict(kv_indptr=None), -1), (dict(kv_indices=None), -1), (dict(out=None), -1),
@@ -328,7 +330,7 @@ def _v4_args(**kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(H=64), -3), (dict(D=576), -3), (dict(max_rows=2049), -3), (dict(N=-1), -2),
+    (dict(H=64), -3), (dict(D=576), -3), (dict(max_rows=2 ** 31 - 1), -2), (dict(N=-1), -2),
     (dict(total_pages=-1), -2), (dict(max_rows=-1), -2),
     (dict(q=None), -1), (dict(out=None), -1), (dict(kv_indptr_prefix=None), -1),
     (dict(kv_indices_extend=None), -1), (dict(unified_kv=None), -1), (dict(kv=None), -1),
@@ -369,7 +371,7 @@ def _prefill_args(**kw):
     (dict(H=32), -3), (dict(N=-1), -2), (dict(topk=-1), -2), (dict(kv_format=3), -4),
     (dict(q=None), -1), (dict(kv=None), -1), (dict(out=None), -1), (dict(indices=None), -1),
     (dict(q_stride_h=100), -7), (dict(out=0x4002), -7), (dict(kv_rows=-3), -2),
-    (dict(kv_stride_row=570), -7), (dict(kv_stride_row=590), -7),
+    (dict(kv_stride_row=570), -7), (dict(kv_stride_row=590), -7), (dict(topk=2 ** 31 - 1), -2),
 ])
 def test_prefill_rejects_bad_arguments(lib, kw, code):
     a = _prefill_args(**kw)
@@ -425,7 +427,7 @@ def _v4fp8_args(**kw):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(H=64), -3), (dict(N=-1), -2), (dict(max_rows=-1), -2), (dict(total_pages=-1), -2),
-    (dict(max_rows=2049), -3),
+    (dict(max_rows=2 ** 31 - 1), -2),
     (dict(q_nope=None), -1), (dict(q_rope=None), -1), (dict(out=None), -1),
     (dict(unified_kv_nope=None), -1), (dict(kv_rope=None), -1), (dict(kv_indices_extend=None), -1),
     (dict(stride_q_nope_h=520), -7), (dict(stride_kv_nope_page=496), -7), (dict(stride_kv_rope_page=60), -7),
@@ -441,3 +443,30 @@ def test_prefill_v4_fp8_empty_is_a_no_op(lib):
     # empty pools need no pool pointers
     a = _v4fp8_args(N=0, total_pages=0, unified_kv_nope=None, unified_kv_rope=None)
     assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(a), None) == 0
+
+
+def test_long_lists_accepted_unsplit(lib):
+    """Lists longer than one 2048-entry chunk run in one workgroup per query:
+    every entry accepts them, unsplit, with no workspace."""
+    rc, ws = _ws(lib, _decode_args(topk=4096, num_splits=1))
+    assert rc == 0 and ws == 0
+    rc, ws = _csr_ws(lib, _csr_args(max_kv_len=200_000, num_splits=1))
+    assert rc == 0 and ws == 0
+    # more than 64 x 2048 entries with automatic splits
+    assert _csr_ws(lib, _csr_args(max_kv_len=200_000))[0] == 0
+    n = ctypes.c_size_t(1)
+    assert lib.dsa_mla_prefill_workspace_size(ctypes.byref(_prefill_args(topk=4096)), ctypes.byref(n)) == 0
+    assert n.value == 0
+    assert lib.dsa_mla_prefill_v4(ctypes.byref(_v4_args(max_rows=1 << 20, N=0)), None) == 0
+    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(_v4fp8_args(max_rows=1 << 20, N=0)), None) == 0
+
+
+def test_max_list_bound(lib):
+    """DSA_MLA_MAX_LIST (header) = abi.MAX_LIST: the longest list accepted; one more is a
+    bad shape (entry positions plus one 2048-entry chunk stay within int32)."""
+    hdr = open(os.path.join(os.path.dirname(abi.LIB_PATH), "..", "..", "include", "dsa_mla.h")).read()
+    assert f"#define DSA_MLA_MAX_LIST {abi.MAX_LIST}" in hdr
+    assert _ws(lib, _decode_args(topk=abi.MAX_LIST, num_splits=1))[0] == 0
+    assert _ws(lib, _decode_args(topk=abi.MAX_LIST + 1, num_splits=1))[0] == -2
+    assert _csr_ws(lib, _csr_args(max_kv_len=abi.MAX_LIST))[0] == 0
+    assert _csr_ws(lib, _csr_args(max_kv_len=abi.MAX_LIST + 1))[0] == -2
