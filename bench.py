@@ -6,7 +6,8 @@ A "step" is one sparse-MLA decode call over one batch of synthetic inputs that
 are already resident in HBM.  Default workload: BASELINE config 3 (the one the
 north-star target is quoted on) - fp8 656-byte KV rows, batch 128, MTP s_q = 2,
 128 heads, top-k 2048, seq_len 65536 paged at 64 rows, causal.  The JSON line
-also carries config 5 (bf16 sparse prefill, 8192 x 128 heads x top-k 2048) in
+also carries configs 1, 2 and 4 (bf16 decode; 1 and 4 timed as HIP-graph
+replays), config 5 (bf16 sparse prefill, 8192 x 128 heads x top-k 2048) in
 TFLOP/s, the same decode on MXFP8 split streams (the reference's own -dtype fp8
 format, C3-shaped: B=128, s_q=2, 2048 rows per token), the DeepSeek-V4
 prefill (bf16 and fp8 rows) at the reference harness's default shape, the
@@ -272,7 +273,7 @@ def cpu_baseline_mx(m, sample_batches):
     t0 = time.perf_counter()
     oracle.mla_decode_mxfp8(*q, *kv, ip, ix, s_q, SM_SCALE, num_threads=nt)
     dt = time.perf_counter() - t0
-    return dict(value=dt * B / nb * 1e6, unit="us/step", cores=nt, kind="port",
+    return dict(value=dt * B / nb * 1e6, unit="us/step", cores=nt, kind="port", cpu_model=cpu_model(),
                 sample=f"{nb} of {B} batches ({nb * s_q} query tokens, all 128 heads), {dt:.2f} s "
                        f"measured, scaled x{B / nb:.1f} to one step")
 
@@ -387,7 +388,7 @@ def cpu_baseline_v4(v, sample):
         oracle.mla_prefill_v4(*args, num_threads=nt)
     dt = time.perf_counter() - t0
     rows = int(ipp[n] + ipe[n])
-    return dict(value=4.0 * H * rows * 512 / dt / 1e12, unit="TFLOP/s", cores=nt, kind="port",
+    return dict(value=4.0 * H * rows * 512 / dt / 1e12, unit="TFLOP/s", cores=nt, kind="port", cpu_model=cpu_model(),
                 sample=f"{n} of {N} queries ({rows} rows), {dt:.2f} s")
 
 
@@ -432,7 +433,7 @@ def cpu_baseline_topk(tk, sample):
     t0 = time.perf_counter()
     oracle.topk_indices(scores, lengths, tk["topk"])
     dt = time.perf_counter() - t0
-    return dict(value=round(dt / n_s * tk["T"] * 1e6, 1), unit="us/step", cores=1, kind="port",
+    return dict(value=round(dt / n_s * tk["T"] * 1e6, 1), unit="us/step", cores=1, kind="port", cpu_model=cpu_model(),
                 sample=f"{n_s} of {tk['T']} tokens, {dt:.2f} s, scaled to the step")
 
 
@@ -443,13 +444,13 @@ def measured_peaks(dev):
     n = 2 << 30
     src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
-    copy_ms = time_steps(lambda: dst.copy_(src), 10, 5)
+    copy_ms = time_steps(lambda: dst.copy_(src), 20, None)
     del src, dst
     m = 8192
     a = torch.randn((m, m), device=dev).to(torch.bfloat16)
     b = torch.randn((m, m), device=dev).to(torch.bfloat16)
     c = torch.empty((m, m), device=dev, dtype=torch.bfloat16)
-    gemm_ms = time_steps(lambda: torch.matmul(a, b, out=c), 10, 5)
+    gemm_ms = time_steps(lambda: torch.matmul(a, b, out=c), 20, None)
     del a, b, c
     torch.cuda.empty_cache()
     return {"hbm_copy_GBps": round(2 * n / (copy_ms * 1e-3) / 1e9, 1),
@@ -573,6 +574,112 @@ def kernel_avg_ms(fn, reps):
     return sum(a.elapsed_time(b) for a, b in evs) / reps
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for the cpu_baseline records."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def reference_figures(T, s_q, V, row_bytes, ms):
+    """The reference harness's own throughput figures (opus_attn/dsa_v32/common/host.cc:
+    301-316): flops = 2 * s_q * H * total_kv * (576 + 512) and bytes = q + o + kv with
+    q = tokens * H * row_bytes, o = tokens * H * 512 * 2, kv = total_kv * row_bytes, where
+    total_kv is the summed per-batch list length (the s_q tokens of a batch share its list
+    there).  Here total_kv = V / s_q.  Unlike the algorithmic bytes, kv counts a row once per
+    batch although each query token gathers its own list, and q counts Q at the KV row width."""
+    total_kv = V / s_q
+    q_b = T * H * row_bytes
+    o_b = T * H * D_VO * 2
+    kv_b = total_kv * row_bytes
+    flops = 2.0 * s_q * H * total_kv * (D_QK + D_VO)
+    return {"q_o_kv_bytes": int(q_b + o_b + kv_b), "TBps": round((q_b + o_b + kv_b) / (ms * 1e-3) / 1e12, 3),
+            "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1)}
+
+
+def graph_replay(make_step, calls):
+    """Capture `calls` back-to-back steps into one HIP graph and return its replay function.
+    For steps of a few microseconds, where timing launches from Python would time the host.
+    `make_step` is called with the capture stream current (the step binds that stream)."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step = make_step()
+        for _ in range(3):
+            step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for _ in range(calls):
+            step()
+    torch.cuda.synchronize()
+    return g.replay, g
+
+
+def decode_leg(name, args, dev):
+    """One decode configuration (c1, c2, c4) as a leg of the JSON line: step time, the fused
+    kernel's roofline, the reference's own figures and the CPU oracle on the same inputs.  c1
+    and c4 (a few microseconds per step) are timed as HIP-graph replays of 20 steps; c2 as
+    stream launches like the headline.  Unsplit, the step is the fused kernel; c4's step also
+    holds the combine kernel, and its roofline is taken over the whole step."""
+    import torch
+    from opfoundry_amd import dsa
+    cfg = CONFIGS[name]
+    d = make_decode(cfg, dev)
+    splits = cfg.get("splits", 0)
+    out, lse = decode_call(d, splits)
+    torch.cuda.synchronize()
+    ref_out, ref_lse = out.clone(), lse.clone()
+    a = dsa.make_decode_args(d["q"], d["kv"], d["idx"], SM_SCALE, out, lse, seq_lens=d["seq_lens"],
+                             block_table=d["block_table"], block_size=d["block_size"],
+                             causal=d["causal"], num_splits=splits, kv_batch_stride=d["kv_batch_stride"])
+    ns = dsa.decode_num_splits(a)
+    ws = torch.empty(max(dsa.decode_workspace_size(a), 1), dtype=torch.uint8, device=dev)
+    graphed = name in ("c1", "c4")
+    if graphed:
+        calls = 20
+        replay, g = graph_replay(lambda: prepared_decode(a, ws), calls)
+        reps = max(5, args.steps // 4)
+        ms = time_steps(replay, reps, args.warmup) / calls
+        timing = f"HIP graph of {calls} steps, replayed {reps} times"
+    else:
+        g = None
+        ms = time_steps(prepared_decode(a, ws), args.steps, args.warmup)
+        timing = f"{args.steps} stream launches"
+    torch.cuda.synchronize()
+    # the replayed / launched steps rewrote out and lse: they must equal the eager call's
+    same = bool(torch.equal(out.view(torch.int16), ref_out.view(torch.int16)) and torch.equal(lse, ref_lse))
+    B, s_q, topk = d["idx"].shape
+    V = count_valid(d)
+    row_bytes = 656 if cfg["fp8"] else 1152
+    T = B * s_q
+    alg_bytes = T * H * D_QK * 2 + V * row_bytes + T * H * D_VO * 2 + T * H * 4 + T * topk * 4
+    ach = alg_bytes / (ms * 1e-3) / 1e9
+    leg = {"workload": f"{name}: {NAMES[name]}", "us_per_step": round(ms * 1e3, 3), "timing": timing,
+           "num_splits": ns, "valid_pairs": V, "replay_equals_eager": same,
+           "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(ach / HBM_PEAK_GBS, 4),
+                        "traffic": profiled_traffic(f"dsa_mla_fwd_bf16_{name}_traffic.txt"),
+                        "kernel": "dsa_mla_fwd_kernel<bf16>" + (" + dsa_mla_combine_kernel (whole step)"
+                                                                 if ns > 1 else ""),
+                        "kernel_avg_us": round(ms * 1e3, 3), "alg_bytes": alg_bytes,
+                        "mfma_frac": round(FLOP_PER_PAIR * V / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)},
+           "reference_figures": reference_figures(T, s_q, V, row_bytes, ms)}
+    del g, a, ws, out, lse
+    if not args.no_cpu:
+        log(f"CPU baseline (oracle) on {name}")
+        leg["cpu_baseline"] = cpu_baseline_decode(d, cfg["fp8"], min(args.cpu_sample, 64), T)
+    del d
+    torch.cuda.empty_cache()
+    return leg
+
+
 # -------------------------------------------------------------- CPU baseline
 
 def cpu_baseline_decode(d, fmt_fp8, sample_queries, unit_scale):
@@ -611,7 +718,7 @@ def cpu_baseline_decode(d, fmt_fp8, sample_queries, unit_scale):
     per_query = dt / len(picks)
     scale = unit_scale / len(picks)
     how = "the whole step" if len(picks) == unit_scale else f"scaled x{scale:.1f} to one step"
-    return dict(value=per_query * unit_scale * 1e6, unit="us/step", cores=nt, kind="port",
+    return dict(value=per_query * unit_scale * 1e6, unit="us/step", cores=nt, kind="port", cpu_model=cpu_model(),
                 sample=f"{len(picks)} of {B * s_q} query tokens (all 128 heads, full top-k), "
                        f"{dt:.2f} s measured, {how}")
 
@@ -631,7 +738,7 @@ def cpu_baseline_prefill(p, sample_queries, total_pairs):
     oracle.mla_prefill(q, kv, idx, SM_SCALE, num_threads=nt)
     dt = time.perf_counter() - t0
     tflops = FLOP_PER_PAIR * pairs / dt / 1e12
-    return dict(value=tflops, unit="TFLOP/s", cores=nt, kind="port",
+    return dict(value=tflops, unit="TFLOP/s", cores=nt, kind="port", cpu_model=cpu_model(),
                 sample=f"{sample_queries} of {N} queries ({pairs} pairs), {dt:.2f} s; "
                        f"full step would take {dt * total_pairs / pairs:.0f} s")
 
@@ -648,6 +755,7 @@ def main():
     ap.add_argument("--config", default="c3", choices=list(CONFIGS),
                     help="decode workload of the JSON line (c5 only with --kernel-only)")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-legs", action="store_true", help="skip the c1 / c2 / c4 decode legs")
     ap.add_argument("--no-mx", action="store_true")
     ap.add_argument("--no-v4", action="store_true")
     ap.add_argument("--no-topk", action="store_true")
@@ -783,11 +891,19 @@ def main():
     }
     del out, lse, ws, step, a
 
+    res["reference_figures"] = reference_figures(B * s_q, s_q, V, row_bytes, ms)
     if not args.no_cpu:
         log("CPU baseline (oracle) on a bounded sample")
         res["cpu_baseline"] = cpu_baseline_decode(d, cfg["fp8"], args.cpu_sample, B * s_q)
     del d
     torch.cuda.empty_cache()
+
+    if not args.no_legs:
+        res["decode_legs"] = {}
+        for name in ("c1", "c2", "c4"):
+            if name != args.config:
+                log(f"decode leg {name}")
+                res["decode_legs"][name] = decode_leg(name, args, dev)
 
     if not args.no_mx:
         log("building mx (MXFP8 split-stream) inputs")
@@ -889,16 +1005,8 @@ def main():
     if not args.no_peaks:
         log("measured peaks (copy, bf16 GEMM)")
         pk = measured_peaks(dev)
+        # information only: every roofline fraction is taken against the spec peaks
         res["measured_peaks"] = pk
-        # fractions against the achievable rates beside the spec ones
-        res["roofline"]["frac_measured"] = round(res["roofline"]["achieved"] / pk["hbm_copy_GBps"], 4)
-        for key in ("mxfp8", "topk"):
-            if key in res:
-                r = res[key]["roofline"]
-                r["frac_measured"] = round(r["achieved"] / pk["hbm_copy_GBps"], 4)
-        for leg in [res.get("prefill")] + list(res.get("v4_prefill", {}).values()):
-            if leg:
-                leg["roofline"]["frac_measured"] = round(leg["roofline"]["achieved"] / pk["bf16_gemm_TFLOPs"], 4)
     print(json.dumps(res))
 
 
