@@ -26,6 +26,12 @@
  * Duplicated positions count once per occurrence.  A (b, t, head) with no
  * valid entry gets O = 0 and LSE = +inf.
  *
+ * Heads.  Every entry takes any head count H >= 1 (H <= 0 is
+ * DSA_ERR_BAD_SHAPE).  A query token runs in ceil(H / 128) workgroups of 128
+ * heads; the last one computes its heads past H on a copy of head H-1 and
+ * stores nothing for them, so outputs, LSEs and partials are written for
+ * heads 0..H-1 only.
+ *
  * Numerics.  Scores s = (q . k) * sm_scale in fp32; softmax probabilities are
  * rounded to bf16 before the P.V product, accumulation is fp32, O is written
  * as bf16 (round to nearest even) and LSE = max + ln(sum exp(s - max)) as
@@ -336,7 +342,7 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* args, void* workspace, size_t wo
  * included.  max_rows bounds the prefix + extend entries of any query (a
  * query with more gets NaN O and LSE, never a silently truncated attention);
  * a list of any length runs in the query's one workgroup, 2048 entries at a
- * time.  H must be 128; total_pages and total_tokens must be below 2^30.
+ * time.  total_pages and total_tokens must be below 2^30.
  */
 typedef struct {
     const void* q;

@@ -249,9 +249,11 @@ struct FwdParams {
     __bf16* out;
     int64_t o_sb, o_st, o_sh;
     float* lse;
-    float* part_o;               // [splits][B*s_q][128][512] fp32, NULL when unsplit
-    float* part_lse;             // [splits][B*s_q][128]
+    float* part_o;               // [splits][B*s_q][H][512] fp32, NULL when unsplit
+    float* part_lse;             // [splits][B*s_q][H]
     int32_t B, s_q, topk, chunk;
+    int32_t H;                   // heads of a query token (any H >= 1)
+    int32_t hgroups;             // workgroups per (query token, split): ceil(H / 128)
     int32_t causal;              // 1: decode rule  j <= L - s_q + t
                                  // 2: prefill rule j <= b + causal_offset
     int64_t causal_offset;
@@ -361,11 +363,18 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     LDS_AS int32_t* const s_rows = (LDS_AS int32_t*)s_rows_arr;
     LDS_AS int* const s_misc = (LDS_AS int*)s_misc_arr;
 
-    const int b = blockIdx.x, t = blockIdx.y, split = blockIdx.z;
+    // blockIdx.x = query token * hgroups + head group
+    const int b = p.hgroups == 1 ? (int)blockIdx.x : (int)blockIdx.x / p.hgroups;
+    const int hbase = p.hgroups == 1 ? 0 : HEADS * ((int)blockIdx.x % p.hgroups);
+    const int t = blockIdx.y, split = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hi = lane >> 5, r32 = lane & 31;
-    const int head = wave * 32 + r32;
+    const int head = wave * 32 + r32;         // head within the group (LDS exchanges)
+    // The query's head: heads past H (H not a multiple of 128) are computed on
+    // a copy of head H-1 and never stored.
+    const int head_g = hbase + head;
+    const int head_q = min(head_g, p.H - 1);
     if (tid == 0) s_misc[4] = 0;
 
     // ---- 0. Q fragments (B operand of S^T = K Q^T): lane -> head r32, k-chunk hi ----
@@ -375,20 +384,20 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     if constexpr (L::MX) {
         // fp8 codes of dims 16ks + 8hi .. +7 in the low half of qf[ks],
         // converted to bf16 once they have landed; RoPE as bf16
-        const unsigned char* q8p = p.q8 + (int64_t)b * p.q8_sb + (int64_t)t * p.q8_st + (int64_t)head * p.q8_sh + 8 * hi;
+        const unsigned char* q8p = p.q8 + (int64_t)b * p.q8_sb + (int64_t)t * p.q8_st + (int64_t)head_q * p.q8_sh + 8 * hi;
 #pragma unroll
         for (int ks = 0; ks < L::Q8_KS; ++ks) {
             const u32x2 c = *reinterpret_cast<const u32x2*>(q8p + 16 * ks);
             qf[ks] = u32x4{c[0], c[1], 0u, 0u};
         }
         q_scales = *reinterpret_cast<const u32x4*>(p.qsc + (int64_t)b * p.qsc_sb + (int64_t)t * p.qsc_st +
-                                                   (int64_t)head * p.qsc_sh);
-        const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head * p.q_sh + 8 * hi;
+                                                   (int64_t)head_q * p.qsc_sh);
+        const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head_q * p.q_sh + 8 * hi;
 #pragma unroll
         for (int ks = L::Q8_KS; ks < L::KS; ++ks)
             qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * (ks - L::Q8_KS));
     } else {
-        const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head * p.q_sh + 8 * hi;
+        const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head_q * p.q_sh + 8 * hi;
 #pragma unroll
         for (int ks = 0; ks < L::KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * ks);
     }
@@ -887,7 +896,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             lt += __shfl_xor(lt, 32, 64);
             float m_fold = m_ref;
             if constexpr (L::D512)
-                if (p.attn_sink) add_sink(lt, m_ref, p.attn_sink[head] * LOG2E, lt, m_fold);
+                if (p.attn_sink) add_sink(lt, m_ref, p.attn_sink[head_q] * LOG2E, lt, m_fold);
             m_ref = m_fold + __builtin_amdgcn_logf(lt);
         }
         // P of both halves, then one barrier: the wave's VALU work does not
@@ -1003,7 +1012,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             lt += __shfl_xor(lt, 32, 64);
             float m_fold = m_ref;
             if constexpr (L::D512)
-                if (p.attn_sink) add_sink(lt, m_ref, p.attn_sink[head] * LOG2E, lt, m_fold);
+                if (p.attn_sink) add_sink(lt, m_ref, p.attn_sink[head_q] * LOG2E, lt, m_fold);
             m_ref = m_fold + __builtin_amdgcn_logf(lt);
         }
         float e[16];
@@ -1153,7 +1162,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     float l = l_rows, m_fin = m_ref, o_scale = 1.0f;
     if constexpr (L::D512)
         if (p.attn_sink) {
-            add_sink(l_rows, m_ref, p.attn_sink[head] * LOG2E, l, m_fin);
+            add_sink(l_rows, m_ref, p.attn_sink[head_q] * LOG2E, l, m_fin);
             o_scale = __builtin_amdgcn_exp2f(m_ref - m_fin);
         }
     const int64_t qrow = (int64_t)b * p.s_q + t;
@@ -1164,10 +1173,11 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     if (hi == 0) s_l[head] = truncated ? __builtin_nanf("") : (has ? (nchunks == 1 && ntiles == 1 ? 1.0f : o_scale / l) : 0.0f);
     if (hi == 0) {
         const float lse_v = truncated ? __builtin_nanf("") : (m_fin + __builtin_amdgcn_logf(l)) * LN2;
-        if (p.part_o == nullptr) {
-            if (p.lse) p.lse[qrow * HEADS + head] = has || truncated ? lse_v : INFINITY;
+        if (head_g >= p.H) {
+        } else if (p.part_o == nullptr) {
+            if (p.lse) p.lse[qrow * p.H + head_g] = has || truncated ? lse_v : INFINITY;
         } else {
-            p.part_lse[((int64_t)split * p.B * p.s_q + qrow) * HEADS + head] = has || truncated ? lse_v : -FLT_MAX;
+            p.part_lse[((int64_t)split * p.B * p.s_q + qrow) * p.H + head_g] = has || truncated ? lse_v : -FLT_MAX;
         }
     }
     __syncthreads();
@@ -1208,8 +1218,9 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 const int r = 8 * wave + k;
+                if (hbase + 32 * h + r >= p.H) break;
                 const u32x4 v = lds_ld<u32x4>(stg + r * OUT_STRIDE + 16 * ln);
-                __bf16* const dst = orow + (int64_t)(32 * h + r) * p.o_sh + 8 * ln;
+                __bf16* const dst = orow + (int64_t)(hbase + 32 * h + r) * p.o_sh + 8 * ln;
                 if (o16) {
                     *reinterpret_cast<u32x4*>(dst) = v;
                 } else {
@@ -1230,7 +1241,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         const int ln = opaque(lane);
         const lds_ptr stg = (wave < 2 ? T0 : T1) + (wave & 1) * 32 * PST;
         const int st_w = opaque(r32 * PST + 16 * hi);
-        const int64_t prow0 = ((int64_t)split * p.B * p.s_q + qrow) * HEADS;
+        const int64_t prow0 = ((int64_t)split * p.B * p.s_q + qrow) * p.H + hbase;
 #pragma unroll
         for (int h = 0; h < NWAVE; ++h) {
 #pragma unroll
@@ -1249,7 +1260,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                 const int r = 2 * k + (ln >> 5);
                 const f32x4 v = lds_ld<f32x4>(stg + r * PST + 16 * (ln & 31));
                 float* op = p.part_o + (prow0 + 32 * h + r) * D_VO + 128 * wave + 4 * (ln & 31);
-                *reinterpret_cast<f32x4*>(op) = v;
+                if (hbase + 32 * h + r < p.H) *reinterpret_cast<f32x4*>(op) = v;
             }
         }
     }
@@ -1422,6 +1433,12 @@ int64_t row_stride_bytes(int fmt, int64_t stride) {
     return stride < 0 || bytes < dense || (bytes % 16) != 0 ? -1 : bytes;
 }
 int ilog2(int v) { int s = 0; while ((1 << s) < v) ++s; return s; }
+// workgroups per query token: 128 heads each (the last group masks heads past H)
+int head_groups(int32_t H) { return (H + HEADS - 1) / HEADS; }
+// any H >= 1; the grid's x extent (query tokens x head groups) stays below 2^31
+bool heads_ok(int32_t H, int64_t tokens) {
+    return H >= 1 && tokens * head_groups(H) <= INT32_MAX;
+}
 
 int auto_splits(int64_t queries, int topk) {
     int ns = 1;
@@ -1438,13 +1455,13 @@ int auto_splits(int64_t queries, int topk) {
 int validate_decode(const dsa_mla_decode_args* a, int* ns_out, int* chunk_out) {
     if (!a) return DSA_ERR_NULL_POINTER;
     if (a->B < 0 || a->s_q <= 0 || a->topk < 0 || a->topk > MAX_LIST) return DSA_ERR_BAD_SHAPE;
-    if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
+    if (!heads_ok(a->H, a->B)) return DSA_ERR_BAD_SHAPE;
     if (a->kv_format != DSA_KV_BF16 && a->kv_format != DSA_KV_FP8_656) return DSA_ERR_BAD_FORMAT;
     if (a->kv_total_rows < 0 || a->kv_total_rows > INT32_MAX) return DSA_ERR_BAD_SHAPE;
     if (a->block_table && a->block_size <= 0) return DSA_ERR_BAD_SHAPE;
     if (row_stride_bytes(a->kv_format, a->kv_stride_row) < 0) return DSA_ERR_BAD_STRIDE;
     if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
-    const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q, a->topk);
+    const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q * head_groups(a->H), a->topk);
     const int chunk = a->topk == 0 ? 0 : (a->topk + ns - 1) / ns;
     if (a->B > 0 && a->topk > 0) {
         if (!a->q || !a->kv_cache || !a->seq_lens || !a->indices || !a->out) return DSA_ERR_NULL_POINTER;
@@ -1464,12 +1481,12 @@ int validate_decode(const dsa_mla_decode_args* a, int* ns_out, int* chunk_out) {
 
 size_t decode_ws_bytes(const dsa_mla_decode_args* a, int ns) {
     if (ns <= 1 || a->B == 0) return 0;
-    const size_t rows = (size_t)a->B * a->s_q * HEADS;
+    const size_t rows = (size_t)a->B * a->s_q * a->H;
     return (size_t)ns * rows * (D_VO + 1) * sizeof(float) + 256;
 }
 
 int launch_fwd(const FwdParams& fp, int fmt, int B, int s_q, int ns, hipStream_t st) {
-    dim3 grid(B, s_q, ns), block(NTHR);
+    dim3 grid((unsigned)((int64_t)B * fp.hgroups), s_q, ns), block(NTHR);
     if (fmt == DSA_KV_BF16) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_BF16>, grid, block, 0, st, fp);
     else if (fmt == DSA_KV_FP8_656) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_FP8_656>, grid, block, 0, st, fp);
     else if (fmt == DSA_KV_MXFP8) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_MXFP8>, grid, block, 0, st, fp);
@@ -1491,11 +1508,11 @@ int validate_csr(const dsa_mla_decode_csr_args* a, int* ns_out, int* chunk_out) 
     if (!a) return DSA_ERR_NULL_POINTER;
     if (a->B < 0 || a->s_q <= 0 || a->max_kv_len < 0 || a->max_kv_len > MAX_LIST || a->total_tokens < 0)
         return DSA_ERR_BAD_SHAPE;
-    if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
+    if (!heads_ok(a->H, a->B)) return DSA_ERR_BAD_SHAPE;
     if (a->kv_format != DSA_KV_BF16 && a->kv_format != DSA_KV_FP8_656) return DSA_ERR_BAD_FORMAT;
     if (row_stride_bytes(a->kv_format, a->stride_kv_page) < 0) return DSA_ERR_BAD_STRIDE;
     if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
-    const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q, a->max_kv_len);
+    const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q * head_groups(a->H), a->max_kv_len);
     const int chunk = a->max_kv_len == 0 ? 0 : (a->max_kv_len + ns - 1) / ns;
     if (a->B > 0) {
         // the kernel reads Q even when every list is empty
@@ -1513,16 +1530,16 @@ int validate_csr(const dsa_mla_decode_csr_args* a, int* ns_out, int* chunk_out) 
     return DSA_OK;
 }
 size_t csr_ws_bytes(const dsa_mla_decode_csr_args* a, int ns) {
-    return ns <= 1 || a->B == 0 ? 0 : (size_t)ns * a->B * a->s_q * HEADS * (D_VO + 1) * sizeof(float) + 256;
+    return ns <= 1 || a->B == 0 ? 0 : (size_t)ns * a->B * a->s_q * a->H * (D_VO + 1) * sizeof(float) + 256;
 }
 
 int validate_mx(const dsa_mla_decode_mxfp8_args* a, int* ns_out, int* chunk_out) {
     if (!a) return DSA_ERR_NULL_POINTER;
     if (a->B < 0 || a->s_q <= 0 || a->max_kv_len < 0 || a->max_kv_len > MAX_LIST || a->total_tokens < 0)
         return DSA_ERR_BAD_SHAPE;
-    if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
+    if (!heads_ok(a->H, a->B)) return DSA_ERR_BAD_SHAPE;
     if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
-    const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q, a->max_kv_len);
+    const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q * head_groups(a->H), a->max_kv_len);
     const int chunk = a->max_kv_len == 0 ? 0 : (a->max_kv_len + ns - 1) / ns;
     if (a->B > 0) {
         // the kernel reads Q even when every list is empty
@@ -1546,7 +1563,7 @@ int validate_mx(const dsa_mla_decode_mxfp8_args* a, int* ns_out, int* chunk_out)
     return DSA_OK;
 }
 size_t mx_ws_bytes(const dsa_mla_decode_mxfp8_args* a, int ns) {
-    return ns <= 1 || a->B == 0 ? 0 : (size_t)ns * a->B * a->s_q * HEADS * (D_VO + 1) * sizeof(float) + 256;
+    return ns <= 1 || a->B == 0 ? 0 : (size_t)ns * a->B * a->s_q * a->H * (D_VO + 1) * sizeof(float) + 256;
 }
 
 }  // namespace
@@ -1622,6 +1639,8 @@ namespace {
 
 int decode_launch(const dsa_mla_decode_args* a, int ns, int chunk, void* ws, hipStream_t st) {
     FwdParams fp{};
+    fp.H = a->H;
+    fp.hgroups = head_groups(a->H);
     fp.q = (const __bf16*)a->q;
     fp.q_sb = a->q_stride_b; fp.q_st = a->q_stride_t; fp.q_sh = a->q_stride_h;
     fp.kv = (const unsigned char*)a->kv_cache;
@@ -1644,13 +1663,13 @@ int decode_launch(const dsa_mla_decode_args* a, int ns, int chunk, void* ws, hip
     fp.causal_offset = 0;
     fp.scale_log2 = a->sm_scale * LOG2E;
     if (ns > 1) {
-        const size_t rows = (size_t)a->B * a->s_q * HEADS;
+        const size_t rows = (size_t)a->B * a->s_q * a->H;
         fp.part_o = (float*)ws;
         fp.part_lse = (float*)((char*)ws + (size_t)ns * rows * D_VO * sizeof(float));
     }
     int r = launch_fwd(fp, a->kv_format, a->B, a->s_q, ns, st);
     if (r || ns == 1) return r;
-    return launch_combine(fp.part_o, fp.part_lse, ns, a->B * a->s_q, HEADS, a->s_q, a->out, a->o_stride_b,
+    return launch_combine(fp.part_o, fp.part_lse, ns, a->B * a->s_q, a->H, a->s_q, a->out, a->o_stride_b,
                           a->o_stride_t, a->o_stride_h, a->lse, st);
 }
 
@@ -1675,6 +1694,8 @@ int dsa_mla_decode_csr(const dsa_mla_decode_csr_args* a, void* ws, size_t ws_byt
     if (a->B == 0) return DSA_OK;
     hipStream_t st = (hipStream_t)stream;
     FwdParams fp{};
+    fp.H = a->H;
+    fp.hgroups = head_groups(a->H);
     fp.q = (const __bf16*)a->q;
     fp.q_sb = (int64_t)a->s_q * a->stride_q_b; fp.q_st = a->stride_q_b; fp.q_sh = a->stride_q_h;
     fp.kv = (const unsigned char*)a->kv;
@@ -1690,13 +1711,13 @@ int dsa_mla_decode_csr(const dsa_mla_decode_csr_args* a, void* ws, size_t ws_byt
     fp.B = a->B; fp.s_q = a->s_q; fp.topk = a->max_kv_len; fp.chunk = chunk;
     fp.scale_log2 = a->softmax_scale * LOG2E;
     if (ns > 1) {
-        const size_t rows = (size_t)a->B * a->s_q * HEADS;
+        const size_t rows = (size_t)a->B * a->s_q * a->H;
         fp.part_o = (float*)ws;
         fp.part_lse = (float*)((char*)ws + (size_t)ns * rows * D_VO * sizeof(float));
     }
     int r = launch_fwd(fp, a->kv_format, a->B, a->s_q, ns, st);
     if (r || ns == 1) return r;
-    return launch_combine(fp.part_o, fp.part_lse, ns, a->B * a->s_q, HEADS, a->s_q, a->out, fp.o_sb, fp.o_st,
+    return launch_combine(fp.part_o, fp.part_lse, ns, a->B * a->s_q, a->H, a->s_q, a->out, fp.o_sb, fp.o_st,
                           fp.o_sh, a->lse, st);
 }
 int dsa_mla_decode_mxfp8_workspace_size(const dsa_mla_decode_mxfp8_args* a, size_t* bytes) {
@@ -1716,6 +1737,8 @@ int dsa_mla_decode_mxfp8(const dsa_mla_decode_mxfp8_args* a, void* ws, size_t ws
     if (a->B == 0) return DSA_OK;
     hipStream_t st = (hipStream_t)stream;
     FwdParams fp{};
+    fp.H = a->H;
+    fp.hgroups = head_groups(a->H);
     const int64_t sq = a->s_q;
     fp.q = (const __bf16*)a->q_rope;
     fp.q_sb = sq * a->stride_q_rope_b; fp.q_st = a->stride_q_rope_b; fp.q_sh = a->stride_q_rope_h;
@@ -1740,13 +1763,13 @@ int dsa_mla_decode_mxfp8(const dsa_mla_decode_mxfp8_args* a, void* ws, size_t ws
     fp.B = a->B; fp.s_q = a->s_q; fp.topk = a->max_kv_len; fp.chunk = chunk;
     fp.scale_log2 = a->softmax_scale * LOG2E;
     if (ns > 1) {
-        const size_t rows = (size_t)a->B * a->s_q * HEADS;
+        const size_t rows = (size_t)a->B * a->s_q * a->H;
         fp.part_o = (float*)ws;
         fp.part_lse = (float*)((char*)ws + (size_t)ns * rows * D_VO * sizeof(float));
     }
     int r = launch_fwd(fp, DSA_KV_MXFP8, a->B, a->s_q, ns, st);
     if (r || ns == 1) return r;
-    return launch_combine(fp.part_o, fp.part_lse, ns, a->B * a->s_q, HEADS, a->s_q, a->out, fp.o_sb, fp.o_st,
+    return launch_combine(fp.part_o, fp.part_lse, ns, a->B * a->s_q, a->H, a->s_q, a->out, fp.o_sb, fp.o_st,
                           fp.o_sh, a->lse, st);
 }
 int dsa_mla_combine(const float* po, const float* pl, int32_t ns, int32_t rows, int32_t H, void* out,
@@ -1762,7 +1785,7 @@ int dsa_mla_combine(const float* po, const float* pl, int32_t ns, int32_t rows, 
 int dsa_mla_prefill_workspace_size(const dsa_mla_prefill_args* a, size_t* bytes) {
     if (!a || !bytes) return DSA_ERR_NULL_POINTER;
     if (a->N < 0 || a->topk < 0 || a->kv_rows < 0) return DSA_ERR_BAD_SHAPE;
-    if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
+    if (!heads_ok(a->H, a->N)) return DSA_ERR_BAD_SHAPE;
     if (a->topk > MAX_LIST) return DSA_ERR_BAD_SHAPE;
     *bytes = 0;
     return DSA_OK;
@@ -1772,7 +1795,7 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* a, void* ws, size_t ws_bytes, vo
     (void)ws; (void)ws_bytes;
     if (!a) return DSA_ERR_NULL_POINTER;
     if (a->N < 0 || a->topk < 0 || a->kv_rows < 0 || a->kv_rows > INT32_MAX) return DSA_ERR_BAD_SHAPE;
-    if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
+    if (!heads_ok(a->H, a->N)) return DSA_ERR_BAD_SHAPE;
     if (a->kv_format != DSA_KV_BF16 && a->kv_format != DSA_KV_FP8_656) return DSA_ERR_BAD_FORMAT;
     if (row_stride_bytes(a->kv_format, a->kv_stride_row) < 0) return DSA_ERR_BAD_STRIDE;
     if (a->topk > MAX_LIST) return DSA_ERR_BAD_SHAPE;
@@ -1782,6 +1805,8 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* a, void* ws, size_t ws_bytes, vo
         return DSA_ERR_BAD_STRIDE;
     if (((uintptr_t)a->q & 15) || ((uintptr_t)a->kv & 15) || ((uintptr_t)a->out & 7)) return DSA_ERR_BAD_STRIDE;
     FwdParams fp{};
+    fp.H = a->H;
+    fp.hgroups = head_groups(a->H);
     fp.q = (const __bf16*)a->q;
     fp.q_sb = a->q_stride_n; fp.q_st = 0; fp.q_sh = a->q_stride_h;
     fp.kv = (const unsigned char*)a->kv;
@@ -1812,7 +1837,8 @@ int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* a, void* stream) {
     if (a->total_pages >= dsa_rows::MAX_POOL_ROWS || a->total_tokens >= dsa_rows::MAX_POOL_ROWS)
         return DSA_ERR_BAD_SHAPE;
     if (a->max_rows > MAX_LIST) return DSA_ERR_BAD_SHAPE;
-    if (a->H != HEADS || a->D != DSA_MLA_D_V4) return DSA_ERR_UNSUPPORTED;
+    if (!heads_ok(a->H, a->N)) return DSA_ERR_BAD_SHAPE;
+    if (a->D != DSA_MLA_D_V4) return DSA_ERR_UNSUPPORTED;
     if (a->N == 0) return DSA_OK;
     if (!a->q || !a->out || !a->kv_indptr_prefix || !a->kv_indices_prefix || !a->kv_indptr_extend ||
         !a->kv_indices_extend)
@@ -1825,6 +1851,8 @@ int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* a, void* stream) {
         ((uintptr_t)a->out & 7))
         return DSA_ERR_BAD_STRIDE;
     FwdParams fp{};
+    fp.H = a->H;
+    fp.hgroups = head_groups(a->H);
     fp.q = (const __bf16*)a->q;
     fp.q_sb = a->stride_qo_n; fp.q_st = 0; fp.q_sh = a->stride_qo_h;
     fp.kv = (const unsigned char*)a->unified_kv;
@@ -1849,7 +1877,7 @@ int dsa_mla_prefill_v4_fp8(const dsa_mla_prefill_v4_fp8_args* a, void* stream) {
     if (a->total_pages >= dsa_rows::MAX_POOL_ROWS || a->total_tokens >= dsa_rows::MAX_POOL_ROWS)
         return DSA_ERR_BAD_SHAPE;
     if (a->max_rows > MAX_LIST) return DSA_ERR_BAD_SHAPE;
-    if (a->H != HEADS) return DSA_ERR_UNSUPPORTED;
+    if (!heads_ok(a->H, a->N)) return DSA_ERR_BAD_SHAPE;
     if (a->N == 0) return DSA_OK;
     if (!a->q_nope || !a->q_rope || !a->out || !a->kv_indptr_prefix || !a->kv_indices_prefix ||
         !a->kv_indptr_extend || !a->kv_indices_extend)
@@ -1868,6 +1896,8 @@ int dsa_mla_prefill_v4_fp8(const dsa_mla_prefill_v4_fp8_args* a, void* stream) {
     for (const void* q : ptrs) if ((uintptr_t)q & 15) return DSA_ERR_BAD_STRIDE;
     if ((uintptr_t)a->out & 7) return DSA_ERR_BAD_STRIDE;
     FwdParams fp{};
+    fp.H = a->H;
+    fp.hgroups = head_groups(a->H);
     fp.q = (const __bf16*)a->q_rope;
     fp.q_sb = a->stride_q_rope_n; fp.q_st = 0; fp.q_sh = a->stride_q_rope_h;
     fp.q8 = (const unsigned char*)a->q_nope;

@@ -142,7 +142,7 @@ def test_workspace_and_split_plan(lib):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(H=64), -3), (dict(H=0), -3), (dict(B=-1), -2), (dict(s_q=0), -2), (dict(topk=-5), -2),
+    (dict(H=0), -2), (dict(H=-1), -2), (dict(B=-1), -2), (dict(s_q=0), -2), (dict(topk=-5), -2),
     (dict(kv_format=7), -4), (dict(num_splits=65), -6), (dict(num_splits=-1), -6),
     (dict(topk=2 ** 31 - 1), -2), (dict(block_size=0), -2),
     (dict(q=None), -1), (dict(indices=None), -1), (dict(seq_lens=None), -1), (dict(out=None), -1),
@@ -167,7 +167,7 @@ def test_decode_rejects_missing_workspace(lib):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(H=64), -3), (dict(B=-1), -2), (dict(q=None), -1), (dict(kv_stride_row=575), -7),
+    (dict(H=0), -2), (dict(B=-1), -2), (dict(q=None), -1), (dict(kv_stride_row=575), -7),
     (dict(topk=2 ** 31 - 1), -2),
     # 64 splits of 2 x 128 rows: 33.6 MB of partials, beyond the 16 MiB scratch
     (dict(B=2, num_splits=64), -9),
@@ -229,7 +229,7 @@ def test_csr_split_plan():
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(H=64), -3), (dict(B=-1), -2), (dict(s_q=0), -2), (dict(max_kv_len=-1), -2),
+    (dict(H=0), -2), (dict(B=-1), -2), (dict(s_q=0), -2), (dict(max_kv_len=-1), -2),
     (dict(total_tokens=-1), -2), (dict(kv_format=9), -4), (dict(num_splits=65), -6),
     (dict(max_kv_len=2 ** 31 - 1), -2),
     (dict(q=None), -1), (dict(kv=None), -1), (dict(kv_indptr=None), -1), (dict(kv_indices=None), -1),
@@ -291,7 +291,7 @@ def test_mxfp8_split_plan(lib):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(H=64), -3), (dict(B=-1), -2), (dict(s_q=0), -2), (dict(max_kv_len=-1), -2),
+    (dict(H=0), -2), (dict(B=-1), -2), (dict(s_q=0), -2), (dict(max_kv_len=-1), -2),
     (dict(total_tokens=-1), -2), (dict(num_splits=65), -6),
     (dict(max_kv_len=2 ** 31 - 1), -2),
     (dict(q_nope=None), -1), (dict(q_scale=None), -1), (dict(q_rope=None), -1),
@@ -330,7 +330,7 @@ def _v4_args(**kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(H=64), -3), (dict(D=576), -3), (dict(max_rows=2 ** 31 - 1), -2), (dict(N=-1), -2),
+    (dict(H=0), -2), (dict(D=576), -3), (dict(max_rows=2 ** 31 - 1), -2), (dict(N=-1), -2),
     (dict(total_pages=-1), -2), (dict(max_rows=-1), -2),
     (dict(q=None), -1), (dict(out=None), -1), (dict(kv_indptr_prefix=None), -1),
     (dict(kv_indices_extend=None), -1), (dict(unified_kv=None), -1), (dict(kv=None), -1),
@@ -368,7 +368,7 @@ def _prefill_args(**kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(H=32), -3), (dict(N=-1), -2), (dict(topk=-1), -2), (dict(kv_format=3), -4),
+    (dict(H=0), -2), (dict(N=-1), -2), (dict(topk=-1), -2), (dict(kv_format=3), -4),
     (dict(q=None), -1), (dict(kv=None), -1), (dict(out=None), -1), (dict(indices=None), -1),
     (dict(q_stride_h=100), -7), (dict(out=0x4002), -7), (dict(kv_rows=-3), -2),
     (dict(kv_stride_row=570), -7), (dict(kv_stride_row=590), -7), (dict(topk=2 ** 31 - 1), -2),
@@ -426,7 +426,7 @@ def _v4fp8_args(**kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(H=64), -3), (dict(N=-1), -2), (dict(max_rows=-1), -2), (dict(total_pages=-1), -2),
+    (dict(H=0), -2), (dict(N=-1), -2), (dict(max_rows=-1), -2), (dict(total_pages=-1), -2),
     (dict(max_rows=2 ** 31 - 1), -2),
     (dict(q_nope=None), -1), (dict(q_rope=None), -1), (dict(out=None), -1),
     (dict(unified_kv_nope=None), -1), (dict(kv_rope=None), -1), (dict(kv_indices_extend=None), -1),
@@ -470,3 +470,23 @@ def test_max_list_bound(lib):
     assert _ws(lib, _decode_args(topk=abi.MAX_LIST + 1, num_splits=1))[0] == -2
     assert _csr_ws(lib, _csr_args(max_kv_len=abi.MAX_LIST))[0] == 0
     assert _csr_ws(lib, _csr_args(max_kv_len=abi.MAX_LIST + 1))[0] == -2
+
+
+@pytest.mark.parametrize("H", [1, 16, 40, 64, 96, 128, 200, 256])
+def test_any_head_count_accepted(lib, H):
+    """Any H >= 1: workgroups of 128 heads, the last masking heads past H.  Split
+    workspaces scale with H."""
+    rc, ws = _ws(lib, _decode_args(H=H, B=2))
+    assert rc == 0 and ws >= 2 * 1 * H * 513 * 4
+    assert _csr_ws(lib, _csr_args(H=H))[0] == 0
+    n = ctypes.c_size_t(1)
+    assert lib.dsa_mla_prefill_workspace_size(ctypes.byref(_prefill_args(H=H)), ctypes.byref(n)) == 0
+    assert lib.dsa_mla_prefill_v4(ctypes.byref(_v4_args(H=H, N=0)), None) == 0
+    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(_v4fp8_args(H=H, N=0)), None) == 0
+
+
+def test_head_groups_bound_the_grid(lib):
+    """Query tokens x head groups (ceil(H / 128)) is the grid's x extent: beyond
+    2^31 - 1 the call is a bad shape."""
+    assert _ws(lib, _decode_args(H=1 << 20, B=1 << 24, num_splits=1))[0] == -2
+    assert _ws(lib, _decode_args(H=1 << 7, B=1 << 24, num_splits=1))[0] == 0
