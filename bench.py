@@ -65,6 +65,8 @@ CONFIGS = {
     # top-k index selection producing the c3 step's lists: 256 query tokens (B=128, s_q=2),
     # causal lengths n - s_q + j + 1; five score sets (320 MB) alternate, above the 256 MB MALL
     "topk": dict(kind="topk", T=256, n=65536, s_q=2, topk=2048, sets=5),
+    # the reference harness's --varlen lists (host.cc:238-261): 8 batches, lengths U[5, 131072]
+    "csr_skew": dict(kind="csr", B=8, s_q=1, s=131072),
 }
 NAMES = {
     "c1": "bf16 sparse MLA decode B=2 H=128 top-k 2048 (256 pad) flat KV 8192",
@@ -80,6 +82,8 @@ NAMES = {
               "65536 pages + window 128, sink"),
     "topk": ("top-k index selection for the c3 step: 256 query tokens (B=128 s_q=2), fp32 scores, "
              "causal lengths up to 65536, top-k 2048 (5 score sets alternate step by step)"),
+    "csr_skew": ("bf16 CSR decode on the reference's --varlen lists: B=8, lengths U[5, 131072], "
+                 "shuffled page table; device work plan against uniform splits"),
 }
 
 
@@ -680,6 +684,101 @@ def decode_leg(name, args, dev):
     return leg
 
 
+def make_csr_skew(cfg, dev, seed=2071):
+    """CSR lists drawn as the reference harness's --varlen mode (init_kv_page_table,
+    opus_attn/dsa_v32/common/host.cc:238-261): each batch's length uniform in [min(5, s), s],
+    kv_indices one shuffled permutation of every row; Q and rows ~N(0,1) bf16."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    B, s_q, s = cfg["B"], cfg["s_q"], cfg["s"]
+    lens = torch.randint(min(5, s), s + 1, (B,), generator=g, device=dev)
+    indptr = torch.zeros(B + 1, dtype=torch.int32, device=dev)
+    indptr[1:] = torch.cumsum(lens, 0).to(torch.int32)
+    total = int(indptr[-1])
+    indices = torch.randperm(total, generator=g, device=dev).to(torch.int32)
+    q = torch.randn((B * s_q, H, D_QK), generator=g, device=dev).to(torch.bfloat16)
+    kv = torch.randn((total, D_QK), generator=g, device=dev).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    return dict(q=q, kv=kv, indptr=indptr, indices=indices, lens=lens.cpu().tolist(), s_q=s_q, total=total)
+
+
+def csr_skew_leg(args, dev):
+    """The skewed CSR batch through the device work plan (automatic splits) and through
+    uniform splits (32 per row: the 256 workgroups the per-row rule gives 8 rows), timed as
+    stream launches in three alternating rounds (the median of each), with the plan's
+    roofline and a CPU oracle sample."""
+    import ctypes
+    import numpy as np
+    import torch
+    from opfoundry_amd import dsa
+    from opfoundry_amd.abi import check, load_library
+    c = make_csr_skew(CONFIGS["csr_skew"], dev)
+    T = c["q"].shape[0]
+    out = torch.empty((T, H, D_VO), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((T, H), dtype=torch.float32, device=dev)
+    lib = load_library()
+    st = torch.cuda.current_stream().cuda_stream
+    steps = {}
+    outs = {}
+    for name, ns in (("plan", 0), ("uniform_32", 32)):
+        a = dsa.make_decode_csr_args(c["q"], c["kv"], c["indptr"], c["indices"], SM_SCALE, out, lse,
+                                     s_q=c["s_q"], max_kv_len=max(c["lens"]), num_splits=ns)
+        n = ctypes.c_size_t(0)
+        check(lib.dsa_mla_decode_csr_workspace_size(ctypes.byref(a), ctypes.byref(n)), "workspace")
+        ws = torch.empty(max(n.value, 1), dtype=torch.uint8, device=dev)
+        ap = ctypes.byref(a)
+
+        def step(ap=ap, ws=ws, nb=n.value):
+            rc = lib.dsa_mla_decode_csr(ap, ws.data_ptr(), nb, st)
+            if rc:
+                check(rc, "dsa_mla_decode_csr")
+        step()
+        torch.cuda.synchronize()
+        outs[name] = (out.clone(), lse.clone())
+        steps[name] = (step, ws, a)
+    # a comparison: three alternating rounds, the median of each
+    times = {name: [] for name in steps}
+    for _ in range(3):
+        for name, (step, _, _) in steps.items():
+            times[name].append(time_steps(step, args.steps, args.warmup))
+    res = {name: sorted(v)[1] for name, v in times.items()}
+    del steps
+    V = c["total"]
+    alg = T * H * D_QK * 2 + V * 1152 + T * H * D_VO * 2 + T * H * 4 + V * 4
+    ms = res["plan"]
+    ach = alg / (ms * 1e-3) / 1e9
+    d_o = (outs["plan"][0].float() - outs["uniform_32"][0].float()).abs().max().item()
+    leg = {"workload": f"csr_skew: {NAMES['csr_skew']}", "lengths": c["lens"],
+           "us_per_step": round(ms * 1e3, 3), "uniform_32_us_per_step": round(res["uniform_32"] * 1e3, 3),
+           "plan_speedup": round(res["uniform_32"] / ms, 3), "plan_vs_uniform_max_abs_dO": d_o,
+           "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                        "kernel": "dsa_csr_plan_kernel + dsa_mla_fwd_kernel<bf16> + dsa_mla_combine_kernel "
+                                  "(whole step)", "kernel_avg_us": round(ms * 1e3, 3), "alg_bytes": alg}}
+    if not args.no_cpu:
+        # the oracle on the first 16384 entries of the longest list, scaled to every entry
+        import oracle
+        b = int(np.argmax(c["lens"]))
+        n = min(16384, c["lens"][b])
+        ip = c["indptr"].cpu().numpy()
+        rows = c["indices"][ip[b]:ip[b] + n].long()
+        q = c["q"][b:b + 1].cpu().view(torch.int16).numpy().view(np.uint16).reshape(1, 1, H, D_QK)
+        kv = c["kv"][rows].cpu().view(torch.int16).numpy().view(np.uint16)
+        idx = np.arange(n, dtype=np.int32).reshape(1, 1, n)
+        nt = oracle.num_threads()
+        t0 = time.perf_counter()
+        oracle.mla_decode(q, kv, idx, np.full(1, n, np.int32), SM_SCALE, num_threads=nt)
+        dt = time.perf_counter() - t0
+        leg["cpu_baseline"] = dict(value=dt * V / n * 1e6, unit="us/step", cores=1, kind="port",
+                                   cpu_model=cpu_model(),
+                                   sample=f"{n} entries of one row ({dt:.2f} s; one row is one oracle task), "
+                                          f"scaled x{V / n:.1f} to the step's {V} entries")
+    del c, out, lse
+    torch.cuda.empty_cache()
+    return leg
+
+
 # -------------------------------------------------------------- CPU baseline
 
 def cpu_baseline_decode(d, fmt_fp8, sample_queries, unit_scale):
@@ -904,6 +1003,8 @@ def main():
             if name != args.config:
                 log(f"decode leg {name}")
                 res["decode_legs"][name] = decode_leg(name, args, dev)
+        log("csr_skew leg (device work plan against uniform splits)")
+        res["csr_skew"] = csr_skew_leg(args, dev)
 
     if not args.no_mx:
         log("building mx (MXFP8 split-stream) inputs")

@@ -209,9 +209,20 @@ int dsa_mla_combine(const float* partial_o, const float* partial_lse, int32_t nu
  * out      : bf16 [B * s_q, H, 512] at out + i * stride_o_b + h * stride_o_h
  * lse      : fp32 [B * s_q, H] dense (may be NULL)
  * max_kv_len: an upper bound of kv_indptr[b + 1] - kv_indptr[b] over b (the
- *            host cannot read the device lists; the split plan uses it).  A
+ *            host cannot read the device lists; it sizes the workspace).  A
  *            query whose list is longer is not truncated silently: its O and
  *            LSE are NaN.
+ * num_splits: 0 = a work plan built on the device from kv_indptr (replacing
+ *            get_mla_metadata, opus_attn/dsa_v32/common/get_mla_metadata.hpp):
+ *            the lists are cut into items of at most `chunk` entries sized so
+ *            that all items fill about 256 workgroups (one round when there
+ *            are fewer than 256 rows), whatever the spread of lengths; a row
+ *            no longer than chunk is one item that writes its output
+ *            directly, a longer row's items write partials that the combine
+ *            merges.  The workspace then holds the plan and at most 512
+ *            partial rows (H x 513 fp32 each), none when max_kv_len <= 128.
+ *            1..DSA_MLA_MAX_SPLITS: every row cut into num_splits equal
+ *            parts (workspace: num_splits partial rows per row; none for 1).
  */
 typedef struct {
     const void* q;
@@ -231,7 +242,7 @@ typedef struct {
     float softmax_scale;
 } dsa_mla_decode_csr_args;
 
-/* Workspace bytes dsa_mla_decode_csr needs (0 when unsplit). */
+/* Workspace bytes dsa_mla_decode_csr needs (0 for num_splits == 1). */
 int dsa_mla_decode_csr_workspace_size(const dsa_mla_decode_csr_args* args, size_t* bytes);
 
 /* Launch the CSR decode (kernel + split combine) on `stream`. */

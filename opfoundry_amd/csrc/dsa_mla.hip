@@ -254,6 +254,11 @@ struct FwdParams {
     int32_t B, s_q, topk, chunk;
     int32_t H;                   // heads of a query token (any H >= 1)
     int32_t hgroups;             // workgroups per (query token, split): ceil(H / 128)
+    // CSR work plan (NULL: one workgroup per (query token, split)): item i =
+    // (query row b * s_q + t, first entry, end entry, partial slot or -1 for a
+    // token the plan left whole); plan_hdr[0] = number of items
+    const int4* plan_items;
+    const int32_t* plan_hdr;
     int32_t causal;              // 1: decode rule  j <= L - s_q + t
                                  // 2: prefill rule j <= b + causal_offset
     int64_t causal_offset;
@@ -363,10 +368,26 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     LDS_AS int32_t* const s_rows = (LDS_AS int32_t*)s_rows_arr;
     LDS_AS int* const s_misc = (LDS_AS int*)s_misc_arr;
 
-    // blockIdx.x = query token * hgroups + head group
-    const int b = p.hgroups == 1 ? (int)blockIdx.x : (int)blockIdx.x / p.hgroups;
+    // blockIdx.x = work item * hgroups + head group.  A work item is query
+    // token b = blockIdx.x, t = blockIdx.y, split blockIdx.z of its list; or,
+    // under a CSR plan, an entry of the plan's item table.
+    const int gx = p.hgroups == 1 ? (int)blockIdx.x : (int)blockIdx.x / p.hgroups;
     const int hbase = p.hgroups == 1 ? 0 : HEADS * ((int)blockIdx.x % p.hgroups);
-    const int t = blockIdx.y, split = blockIdx.z;
+    int b = gx, t = blockIdx.y;
+    const int split = blockIdx.z;
+    int item_k0 = 0, item_k1 = 0, item_slot = -1;
+    if (p.plan_items) {
+        // the grid covers the most items a plan can hold: past the plan's
+        // count the whole workgroup leaves before any barrier
+        if (gx >= __builtin_amdgcn_readfirstlane(p.plan_hdr[0])) return;
+        const int4 w = p.plan_items[gx];
+        const int qrow_i = __builtin_amdgcn_readfirstlane(w.x);
+        b = qrow_i / p.s_q;
+        t = qrow_i - b * p.s_q;
+        item_k0 = __builtin_amdgcn_readfirstlane(w.y);
+        item_k1 = __builtin_amdgcn_readfirstlane(w.z);
+        item_slot = __builtin_amdgcn_readfirstlane(w.w);
+    }
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hi = lane >> 5, r32 = lane & 31;
@@ -409,7 +430,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // (s_q - 1 - t), the reference's count-based MTP causality
     // (opus_attn/dsa_v32/common/host.cc:524-526); a row outside the cache is
     // skipped.
-    const int k0 = split * p.chunk;
+    const int k0 = p.plan_items ? item_k0 : split * p.chunk;
     int k1;
     int64_t jmax = 0;
     const int32_t* idx;
@@ -430,7 +451,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     } else if (p.kv_indptr) {
         const int64_t kb = p.kv_indptr[b];
         const int64_t count = (int64_t)p.kv_indptr[b + 1] - kb - (p.s_q - 1 - t);
-        k1 = (int)min((int64_t)k0 + p.chunk, count);
+        k1 = (int)min(p.plan_items ? (int64_t)item_k1 : (int64_t)k0 + p.chunk, count);
         truncated = count > k_cap;
         idx = p.kv_indices + kb;
     } else {
@@ -1166,6 +1187,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             o_scale = __builtin_amdgcn_exp2f(m_ref - m_fin);
         }
     const int64_t qrow = (int64_t)b * p.s_q + t;
+    // partial results (fp32 O, LSE) in row part_row of the workspace, or the
+    // final bf16 O and LSE
+    const bool to_part = p.part_o != nullptr && (p.plan_items == nullptr || item_slot >= 0);
+    const int64_t part_row = p.plan_items ? (int64_t)item_slot : (int64_t)split * p.B * p.s_q + qrow;
     LDS_AS float* const s_l = (LDS_AS float*)PX;      // P buffer is free now
     // one tile: P is normalised.  A list longer than the caller's bound
     // (max_kv_len / max_rows) was cut: its outputs are NaN, never a silently
@@ -1174,10 +1199,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     if (hi == 0) {
         const float lse_v = truncated ? __builtin_nanf("") : (m_fin + __builtin_amdgcn_logf(l)) * LN2;
         if (head_g >= p.H) {
-        } else if (p.part_o == nullptr) {
+        } else if (!to_part) {
             if (p.lse) p.lse[qrow * p.H + head_g] = has || truncated ? lse_v : INFINITY;
         } else {
-            p.part_lse[((int64_t)split * p.B * p.s_q + qrow) * p.H + head_g] = has || truncated ? lse_v : -FLT_MAX;
+            p.part_lse[part_row * p.H + head_g] = has || truncated ? lse_v : -FLT_MAX;
         }
     }
     __syncthreads();
@@ -1185,7 +1210,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 #pragma unroll
     for (int h = 0; h < NWAVE; ++h) inv[h] = s_l[32 * h + r32];
     const int d0 = 128 * wave + 4 * hi;   // this lane's first output dim in block (m, g)
-    if (p.part_o == nullptr) {
+    if (!to_part) {
         // O through LDS, 32 heads at a time (the heads of o[4m + h]), so that
         // every global store of a wave writes one whole 1 KB head row: written
         // straight from the accumulators, each store would scatter 16-byte
@@ -1241,7 +1266,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         const int ln = opaque(lane);
         const lds_ptr stg = (wave < 2 ? T0 : T1) + (wave & 1) * 32 * PST;
         const int st_w = opaque(r32 * PST + 16 * hi);
-        const int64_t prow0 = ((int64_t)split * p.B * p.s_q + qrow) * p.H + hbase;
+        const int64_t prow0 = part_row * p.H + hbase;
 #pragma unroll
         for (int h = 0; h < NWAVE; ++h) {
 #pragma unroll
@@ -1273,34 +1298,149 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 // O = sum w_i O_i / sum w_i, LSE = m + ln sum w_i (+inf when all are empty).
 // grid = (rows, ceil(H / 4)), block = 256.
 // ---------------------------------------------------------------------------
-static_assert(DSA_MLA_MAX_SPLITS <= 64, "the combine holds one split's LSE per lane");
+// ---------------------------------------------------------------------------
+// CSR work plan: one workgroup of 1024 threads, on the device (the host cannot
+// read the lists).  Query row q = b * s_q + t attends
+// L_q = kv_indptr[b+1] - kv_indptr[b] - (s_q - 1 - t) entries (count-based
+// MTP causality).  The plan cuts the lists into work items of at most
+// `chunk` entries, chunk = max(PLAN_MIN_CHUNK, total / (PLAN_TARGET - rows))
+// (total / PLAN_TARGET from PLAN_TARGET rows on) rounded up to a tile, so
+// that the items of all rows together fill about PLAN_TARGET workgroups,
+// in one round when there are fewer rows, however the lengths are spread:
+// a long list spreads over many workgroups, a short one stays whole.  A row no longer than chunk
+// is one item that writes its output directly; a longer row's items write
+// consecutive partial rows, listed in `splits` for the combine.  Bounds:
+// items <= rows + PLAN_TARGET, split rows < PLAN_TARGET, partial rows
+// < 2 * PLAN_TARGET.  A row longer than max_len is one empty item, which the
+// forward kernel marks cut (NaN).  This takes the place of the reference's
+// get_mla_metadata_kernel (opus_attn/dsa_v32/common/get_mla_metadata.hpp:
+// 8-158), which packs per-CU payloads serially; here equal-sized items are
+// left to the hardware dispatcher.
+// hdr[0] = items, hdr[1] = split rows, hdr[2] = chunk.
+// ---------------------------------------------------------------------------
+constexpr int PLAN_TARGET = 256;     // workgroups a plan aims at: one per CU
+constexpr int PLAN_MIN_CHUNK = 128;  // entries: at least four tiles per item
+constexpr int PLAN_THREADS = 1024;
+
+__global__ void __launch_bounds__(PLAN_THREADS)
+dsa_csr_plan_kernel(const int32_t* __restrict__ indptr, int B, int s_q, int max_len, int4* __restrict__ items,
+                    int4* __restrict__ splits, int32_t* __restrict__ hdr) {
+    constexpr int NW = PLAN_THREADS / 64;
+    __shared__ long long s_tot[NW];
+    __shared__ int s_scan[3][NW];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rows = B * s_q;
+    // entries of row q; -1 for a row longer than max_len
+    auto len_of = [&](int q) -> int {
+        const int b = q / s_q, t = q - b * s_q;
+        const int64_t L = (int64_t)indptr[b + 1] - indptr[b] - (s_q - 1 - t);
+        return L > max_len ? -1 : (int)max(L, (int64_t)0);
+    };
+    long long tot = 0;
+    for (int q = tid; q < rows; q += PLAN_THREADS) tot += max(len_of(q), 0);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) tot += __shfl_xor(tot, off, 64);
+    if (lane == 0) s_tot[wave] = tot;
+    __syncthreads();
+    long long total = 0;
+    for (int w = 0; w < NW; ++w) total += s_tot[w];
+    // Fewer rows than PLAN_TARGET: every row's last item may be partly empty,
+    // so chunk >= total / (PLAN_TARGET - rows) keeps all items in one round of
+    // PLAN_TARGET workgroups (items <= total / chunk + rows).
+    const long long slots = rows < PLAN_TARGET ? PLAN_TARGET - rows : PLAN_TARGET;
+    long long c64 = max((long long)PLAN_MIN_CHUNK, (total + slots - 1) / slots);
+    c64 = (c64 + TILE - 1) / TILE * TILE;
+    const int chunk = (int)min(c64, (long long)MAX_LIST);
+    auto wave_incl = [&](int v) {
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int u = __shfl_up(v, off, 64);
+            if (lane >= off) v += u;
+        }
+        return v;
+    };
+    int item_base = 0, slot_base = 0, split_base = 0;
+    for (int q0 = 0; q0 < rows; q0 += PLAN_THREADS) {
+        const int q = q0 + tid;
+        int L = 0, n = 0;
+        if (q < rows) {
+            L = len_of(q);
+            n = L <= chunk ? 1 : (L + chunk - 1) / chunk;
+        }
+        const int ns = n > 1 ? n : 0, sp = n > 1 ? 1 : 0;
+        const int ia = wave_incl(n), ic = wave_incl(ns), id = wave_incl(sp);
+        if (lane == 63) {
+            s_scan[0][wave] = ia;
+            s_scan[1][wave] = ic;
+            s_scan[2][wave] = id;
+        }
+        __syncthreads();
+        int wa = 0, wc = 0, wd = 0, ta = 0, tc = 0, td = 0;
+        for (int w = 0; w < NW; ++w) {
+            const int x = s_scan[0][w], y = s_scan[1][w], z = s_scan[2][w];
+            if (w < wave) { wa += x; wc += y; wd += z; }
+            ta += x; tc += y; td += z;
+        }
+        const int ib = item_base + wa + ia - n;
+        const int sb = slot_base + wc + ic - ns;
+        const int pb = split_base + wd + id - sp;
+        for (int j = 0; j < n; ++j) {
+            const int e0 = L < 0 ? 0 : j * chunk;
+            const int e1 = L < 0 ? 0 : (int)min((int64_t)(j + 1) * chunk, (int64_t)L);
+            items[ib + j] = make_int4(q, e0, e1, n > 1 ? sb + j : -1);
+        }
+        if (n > 1) splits[pb] = make_int4(q, sb, n, 0);
+        item_base += ta;
+        slot_base += tc;
+        split_base += td;
+        __syncthreads();    // s_scan is rewritten by the next round
+    }
+    if (tid == 0) {
+        hdr[0] = item_base;
+        hdr[1] = split_base;
+        hdr[2] = chunk;
+    }
+}
+
 __global__ void __launch_bounds__(256)
 dsa_mla_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_lse, int ns,
                        int rows, int H, int s_q, __bf16* __restrict__ out, int64_t o_sb, int64_t o_st,
-                       int64_t o_sh, float* __restrict__ lse) {
-    const int row = blockIdx.x;
+                       int64_t o_sh, float* __restrict__ lse, const int4* __restrict__ map,
+                       const int32_t* __restrict__ hdr) {
+    int row = blockIdx.x;
     const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (head >= H) return;
-    const int64_t stride = (int64_t)rows * H;
+    // uniform splits: split s of row r is partial row s * rows + r.  A CSR
+    // plan lists its split query rows instead: (query row, first partial
+    // row, count) with consecutive partial rows; hdr[1] rows are listed.
+    int64_t first = row, step_rows = rows;
+    if (map) {
+        if (row >= hdr[1]) return;
+        const int4 m = map[row];
+        row = m.x;
+        first = m.y;
+        ns = m.z;
+        step_rows = 1;
+    }
+    const int64_t stride = step_rows * H;
+    const int64_t base = first * H + head;     // partial index of split 0
     const int64_t rh = (int64_t)row * H + head;
-    // lane s holds split s's LSE (ns <= 64)
-    const float ls = lane < ns ? part_lse[lane * stride + rh] : -FLT_MAX;
-    float m = ls;
+    float m = -FLT_MAX;
+    for (int s = lane; s < ns; s += 64) m = fmaxf(m, part_lse[s * stride + base]);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    // an empty split (-FLT_MAX) weighs 0; a NaN LSE (a list cut short) makes
-    // the row NaN
-    const float w_lane = ls > -FLT_MAX || ls != ls ? __builtin_amdgcn_exp2f((ls - m) * LOG2E) : 0.0f;
     f32x4 acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
     float den = 0.0f;
     // eight splits' loads in flight at a time; sums in split order
     for (int s0 = 0; s0 < ns; s0 += 8) {
+        float ls[8];
         f32x4 v[8][2];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             if (s0 + j < ns) {
-                const f32x4* src = reinterpret_cast<const f32x4*>(part_o + ((s0 + j) * stride + rh) * D_VO + 8 * lane);
+                ls[j] = part_lse[(s0 + j) * stride + base];
+                const f32x4* src = reinterpret_cast<const f32x4*>(part_o + ((s0 + j) * stride + base) * D_VO + 8 * lane);
                 v[j][0] = src[0];
                 v[j][1] = src[1];
             }
@@ -1308,7 +1448,9 @@ dsa_mla_combine_kernel(const float* __restrict__ part_o, const float* __restrict
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             if (s0 + j < ns) {
-                const float w = __shfl(w_lane, s0 + j, 64);
+                // an empty split (-FLT_MAX) weighs 0; a NaN LSE (a list cut
+                // short) makes the row NaN
+                const float w = ls[j] > -FLT_MAX || ls[j] != ls[j] ? __builtin_amdgcn_exp2f((ls[j] - m) * LOG2E) : 0.0f;
                 den += w;
                 acc0 += w * v[j][0];
                 acc1 += w * v[j][1];
@@ -1500,7 +1642,59 @@ int launch_combine(const float* po, const float* pl, int ns, int rows, int H, in
     if (rows == 0) return DSA_OK;
     dim3 grid(rows, (H + 3) / 4), block(256);
     hipLaunchKernelGGL(dsa_mla_combine_kernel, grid, block, 0, st, po, pl, ns, rows, H, s_q, (__bf16*)out, o_sb,
-                       o_st, o_sh, lse);
+                       o_st, o_sh, lse, (const int4*)nullptr, (const int32_t*)nullptr);
+    return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_HIP;
+}
+
+// Workspace of a CSR work plan: header, item table, split-row map, then the
+// partial rows (fp32 O, then LSE).  A row is split only when it is longer than
+// the plan's chunk (>= PLAN_MIN_CHUNK entries), and a plan never holds more than
+// 2 * PLAN_TARGET partial rows.
+struct CsrPlanLayout {
+    size_t items, map, po, pl, total;
+    int items_max, slots_max;
+};
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+CsrPlanLayout csr_plan_layout(int B, int s_q, int H, int max_len) {
+    CsrPlanLayout L{};
+    const int64_t rows = (int64_t)B * s_q;
+    L.items_max = (int)(rows + PLAN_TARGET);
+    const int64_t per_row = ((int64_t)max_len + PLAN_MIN_CHUNK - 1) / PLAN_MIN_CHUNK;
+    L.slots_max = max_len > PLAN_MIN_CHUNK ? (int)std::min<int64_t>(2 * PLAN_TARGET, rows * per_row) : 0;
+    L.items = 256;
+    L.map = align256(L.items + (size_t)L.items_max * sizeof(int4));
+    L.po = align256(L.map + (size_t)PLAN_TARGET * sizeof(int4));
+    L.pl = align256(L.po + (size_t)L.slots_max * H * D_VO * sizeof(float));
+    L.total = align256(L.pl + (size_t)L.slots_max * H * sizeof(float));
+    return L;
+}
+// the plan's grid: (rows + PLAN_TARGET) x head groups workgroups
+bool plan_grid_ok(int B, int s_q, int H) {
+    return ((int64_t)B * s_q + PLAN_TARGET) * head_groups(H) <= INT32_MAX - PLAN_THREADS;
+}
+// plan kernel, forward kernel over the plan's items, combine of the split rows
+int csr_plan_launch(FwdParams& fp, int fmt, int max_len, void* ws, hipStream_t st) {
+    const CsrPlanLayout L = csr_plan_layout(fp.B, fp.s_q, fp.H, max_len);
+    char* w = (char*)ws;
+    int32_t* hdr = (int32_t*)w;
+    int4* items = (int4*)(w + L.items);
+    int4* map = (int4*)(w + L.map);
+    hipLaunchKernelGGL(dsa_csr_plan_kernel, dim3(1), dim3(PLAN_THREADS), 0, st, fp.kv_indptr, fp.B, fp.s_q, max_len,
+                       items, map, hdr);
+    if (hipGetLastError() != hipSuccess) return DSA_ERR_HIP;
+    fp.plan_items = items;
+    fp.plan_hdr = hdr;
+    fp.chunk = max_len;      // one launch "split": lists longer than max_len are cut
+    if (L.slots_max) {
+        fp.part_o = (float*)(w + L.po);
+        fp.part_lse = (float*)(w + L.pl);
+    }
+    const int r = launch_fwd(fp, fmt, L.items_max, 1, 1, st);
+    if (r || !L.slots_max) return r;
+    dim3 grid(PLAN_TARGET, (fp.H + 3) / 4), block(256);
+    hipLaunchKernelGGL(dsa_mla_combine_kernel, grid, block, 0, st, (const float*)fp.part_o, (const float*)fp.part_lse,
+                       0, 0, fp.H, fp.s_q, fp.out, fp.o_sb, fp.o_st, fp.o_sh, fp.lse, (const int4*)map,
+                       (const int32_t*)hdr);
     return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_HIP;
 }
 
@@ -1512,8 +1706,10 @@ int validate_csr(const dsa_mla_decode_csr_args* a, int* ns_out, int* chunk_out) 
     if (a->kv_format != DSA_KV_BF16 && a->kv_format != DSA_KV_FP8_656) return DSA_ERR_BAD_FORMAT;
     if (row_stride_bytes(a->kv_format, a->stride_kv_page) < 0) return DSA_ERR_BAD_STRIDE;
     if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
-    const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q * head_groups(a->H), a->max_kv_len);
-    const int chunk = a->max_kv_len == 0 ? 0 : (a->max_kv_len + ns - 1) / ns;
+    // num_splits 0: the device work plan (ns 0 below); else uniform splits
+    const int ns = a->num_splits;
+    if (ns == 0 && !plan_grid_ok(a->B, a->s_q, a->H)) return DSA_ERR_BAD_SHAPE;
+    const int chunk = a->max_kv_len == 0 || ns == 0 ? a->max_kv_len : (a->max_kv_len + ns - 1) / ns;
     if (a->B > 0) {
         // the kernel reads Q even when every list is empty
         if (!a->out || !a->kv_indptr || !a->q) return DSA_ERR_NULL_POINTER;
@@ -1530,7 +1726,9 @@ int validate_csr(const dsa_mla_decode_csr_args* a, int* ns_out, int* chunk_out) 
     return DSA_OK;
 }
 size_t csr_ws_bytes(const dsa_mla_decode_csr_args* a, int ns) {
-    return ns <= 1 || a->B == 0 ? 0 : (size_t)ns * a->B * a->s_q * a->H * (D_VO + 1) * sizeof(float) + 256;
+    if (a->B == 0) return 0;
+    if (ns == 0) return csr_plan_layout(a->B, a->s_q, a->H, a->max_kv_len).total;
+    return ns == 1 ? 0 : (size_t)ns * a->B * a->s_q * a->H * (D_VO + 1) * sizeof(float) + 256;
 }
 
 int validate_mx(const dsa_mla_decode_mxfp8_args* a, int* ns_out, int* chunk_out) {
@@ -1539,8 +1737,10 @@ int validate_mx(const dsa_mla_decode_mxfp8_args* a, int* ns_out, int* chunk_out)
         return DSA_ERR_BAD_SHAPE;
     if (!heads_ok(a->H, a->B)) return DSA_ERR_BAD_SHAPE;
     if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
-    const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q * head_groups(a->H), a->max_kv_len);
-    const int chunk = a->max_kv_len == 0 ? 0 : (a->max_kv_len + ns - 1) / ns;
+    // num_splits 0: the device work plan (ns 0 below); else uniform splits
+    const int ns = a->num_splits;
+    if (ns == 0 && !plan_grid_ok(a->B, a->s_q, a->H)) return DSA_ERR_BAD_SHAPE;
+    const int chunk = a->max_kv_len == 0 || ns == 0 ? a->max_kv_len : (a->max_kv_len + ns - 1) / ns;
     if (a->B > 0) {
         // the kernel reads Q even when every list is empty
         if (!a->out || !a->kv_indptr || !a->q_nope || !a->q_scale || !a->q_rope) return DSA_ERR_NULL_POINTER;
@@ -1563,7 +1763,9 @@ int validate_mx(const dsa_mla_decode_mxfp8_args* a, int* ns_out, int* chunk_out)
     return DSA_OK;
 }
 size_t mx_ws_bytes(const dsa_mla_decode_mxfp8_args* a, int ns) {
-    return ns <= 1 || a->B == 0 ? 0 : (size_t)ns * a->B * a->s_q * a->H * (D_VO + 1) * sizeof(float) + 256;
+    if (a->B == 0) return 0;
+    if (ns == 0) return csr_plan_layout(a->B, a->s_q, a->H, a->max_kv_len).total;
+    return ns == 1 ? 0 : (size_t)ns * a->B * a->s_q * a->H * (D_VO + 1) * sizeof(float) + 256;
 }
 
 }  // namespace
@@ -1710,6 +1912,7 @@ int dsa_mla_decode_csr(const dsa_mla_decode_csr_args* a, void* ws, size_t ws_byt
     fp.lse = a->lse;
     fp.B = a->B; fp.s_q = a->s_q; fp.topk = a->max_kv_len; fp.chunk = chunk;
     fp.scale_log2 = a->softmax_scale * LOG2E;
+    if (ns == 0) return csr_plan_launch(fp, a->kv_format, a->max_kv_len, ws, st);
     if (ns > 1) {
         const size_t rows = (size_t)a->B * a->s_q * a->H;
         fp.part_o = (float*)ws;
@@ -1762,6 +1965,7 @@ int dsa_mla_decode_mxfp8(const dsa_mla_decode_mxfp8_args* a, void* ws, size_t ws
     fp.lse = a->lse;
     fp.B = a->B; fp.s_q = a->s_q; fp.topk = a->max_kv_len; fp.chunk = chunk;
     fp.scale_log2 = a->softmax_scale * LOG2E;
+    if (ns == 0) return csr_plan_launch(fp, DSA_KV_MXFP8, a->max_kv_len, ws, st);
     if (ns > 1) {
         const size_t rows = (size_t)a->B * a->s_q * a->H;
         fp.part_o = (float*)ws;

@@ -220,12 +220,21 @@ def test_row_strides_accepted(lib):
 
 
 def test_csr_split_plan():
+    """Automatic splits of the CSR entry: a device work plan whose workspace holds the
+    plan (header, item table, split-row map) and at most 512 partial rows."""
     lib = abi.load_library()
-    # few queries: the planner splits the lists to fill the chip
+    row = 128 * 513 * 4                    # one partial row: H x (512 + 1) fp32
+    # B = 4, s_q = 2, lists up to 3000: 8 rows x ceil(3000 / 128) items bound the partials
     rc, ws = _csr_ws(lib, _csr_args())
-    assert rc == 0 and ws >= 2 * 4 * 2 * 128 * 513 * 4
-    rc, ws1 = _csr_ws(lib, _csr_args(max_kv_len=2048, B=512, s_q=1))
-    assert rc == 0 and ws1 == 0
+    assert rc == 0 and 8 * 24 * row <= ws < 8 * 24 * row + (1 << 16)
+    # lists no longer than 128 entries are never split: no partial rows
+    rc, ws_short = _csr_ws(lib, _csr_args(max_kv_len=128, B=512, s_q=1))
+    assert rc == 0 and ws_short < (1 << 16)
+    # however many rows, at most 2 x 256 partial rows
+    rc, ws_big = _csr_ws(lib, _csr_args(max_kv_len=2048, B=100_000, s_q=1))
+    assert rc == 0 and ws_big < 512 * row + (100_000 + 512) * 16 + (1 << 16)
+    # one explicit split: no workspace
+    assert _csr_ws(lib, _csr_args(num_splits=1)) == (0, 0)
 
 
 @pytest.mark.parametrize("kw,code", [
@@ -284,8 +293,10 @@ def _mx_ws(lib, a):
 def test_mxfp8_split_plan(lib):
     rc, ws = _mx_ws(lib, _mx_args())
     assert rc == 0 and ws >= 2 * 4 * 2 * 128 * 513 * 4
-    rc, ws1 = _mx_ws(lib, _mx_args(max_kv_len=1024, B=128, s_q=2))
-    assert rc == 0 and ws1 == 0
+    # automatic splits are the device work plan; one explicit split needs no workspace
+    assert _mx_ws(lib, _mx_args(max_kv_len=1024, B=128, s_q=2, num_splits=1)) == (0, 0)
+    rc, ws_plan = _mx_ws(lib, _mx_args(max_kv_len=1024, B=128, s_q=2))
+    assert rc == 0 and ws_plan <= 512 * 128 * 513 * 4 + (1 << 16)
     # the reference harness pads the scale stream to 32 bytes per row: accepted
     assert _mx_ws(lib, _mx_args(stride_kv_scale_page=32))[0] == 0
 

@@ -172,3 +172,58 @@ def test_csr_list_longer_than_bound_is_nan(dev, ns):
     lse = lse.cpu().numpy()
     assert np.isnan(lse[0]).all() and torch.isnan(out[0].float()).all()
     assert_parity(bits(out)[1:], lse[1:], o_ref[1:], l_ref[1:], "csr bound: intact query")
+
+
+def test_csr_plan_invariants(dev):
+    """The device work plan of an automatic-split CSR call, read back from the workspace
+    (header at 0, item table at 256, split-row map after it, 256-byte aligned):
+    - chunk = max(128, ceil(total entries / (256 - rows))) rounded up to 32 (fewer than
+      256 rows), and at most 256 items;
+    - each row's items are consecutive and cover [0, L) in chunk-sized pieces
+      (one empty item for an empty row);
+    - a row no longer than chunk writes directly (slot -1); a longer row's items use
+      consecutive partial rows, listed once in the split map;
+    - fewer than 256 split rows and 512 partial rows."""
+    lens, s_q = [40_000, 5, 0, 3_000, 700, 129], 2
+    q, kv, indptr, indices = csr_case(91, lens, s_q, 60_000)
+    o_ref, l_ref = oracle_csr(q, kv, indptr, indices, s_q)
+    out, lse = dsa.mla_decode_csr(t16(q, dev), t16(kv, dev), torch.from_numpy(indptr).to(dev),
+                                  torch.from_numpy(indices).to(dev), SM_SCALE, s_q=s_q)
+    torch.cuda.synchronize()
+    assert_parity(bits(out), lse.cpu().numpy(), o_ref, l_ref, "csr plan")
+    # run again with a workspace we keep, to read the plan
+    rows = len(lens) * s_q
+    ws = torch.zeros(256 << 20, dtype=torch.uint8, device=dev)   # above the plan workspace (134 MB)
+    out2, lse2 = dsa.mla_decode_csr(t16(q, dev), t16(kv, dev), torch.from_numpy(indptr).to(dev),
+                                    torch.from_numpy(indices).to(dev), SM_SCALE, s_q=s_q, workspace=ws)
+    torch.cuda.synchronize()
+    assert (bits(out2) == bits(out)).all()
+    w = ws.cpu().numpy()
+    hdr = w[:12].view(np.int32)
+    n_items, n_split, chunk = (int(x) for x in hdr)
+    L = [max(0, lens[q_ // s_q] - (s_q - 1 - q_ % s_q)) for q_ in range(rows)]
+    total = sum(L)
+    want = max(128, -(-total // (256 - rows)))
+    assert chunk == -(-want // 32) * 32
+    assert n_items <= 256
+    items = w[256:256 + 16 * n_items].view(np.int32).reshape(n_items, 4)
+    items_max = rows + 256
+    map_off = (256 + 16 * items_max + 255) // 256 * 256
+    smap = w[map_off:map_off + 16 * n_split].view(np.int32).reshape(n_split, 4)
+    pos, slots, split_rows = 0, [], []
+    for r in range(rows):
+        n = 1 if L[r] <= chunk else -(-L[r] // chunk)
+        mine = items[pos:pos + n]
+        pos += n
+        assert (mine[:, 0] == r).all()
+        if n == 1:
+            assert tuple(mine[0, 1:]) == (0, L[r], -1)
+        else:
+            assert (mine[:, 1] == np.arange(n) * chunk).all()
+            assert (mine[:, 2] == np.minimum((np.arange(n) + 1) * chunk, L[r])).all()
+            assert (np.diff(mine[:, 3]) == 1).all()
+            slots += list(mine[:, 3])
+            split_rows.append((r, int(mine[0, 3]), n))
+    assert pos == n_items
+    assert [tuple(x[:3]) for x in smap] == split_rows
+    assert len(split_rows) < 256 and len(slots) < 512 and sorted(slots) == list(range(len(slots)))

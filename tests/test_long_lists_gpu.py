@@ -11,7 +11,9 @@ entries (which run one workgroup per query) take lists of any length:
 - the same two lists on the fp8 V4 entry;
 - the V3.2 prefill at top-k 4096 (config-5 shape with twice the list): query t
   attends min(4096, t + 1) distinct positions <= t, -1 padded;
-- a CSR decode list longer than 64 splits x 2048 entries.
+- a skewed CSR batch: one 200,000-row list (longer than 64 splits x 2048
+  entries) beside short and empty ones, through the device work plan and
+  through uniform splits.
 
 Extra cases: a chunk with no valid row between two valid ones, invalid entries
 straddling a chunk boundary, and a query whose only valid rows lie in its
@@ -147,36 +149,43 @@ def test_prefill_topk4096(dev, fp8):
 
 
 def test_csr_decode_beyond_64_chunks(dev):
-    """One CSR list of 140,000 rows (more than 64 splits x 2048 entries) and a
-    short one, automatic and explicit splits."""
+    """A skewed CSR batch: one list of 200,000 rows (more than 64 splits x 2048
+    entries) beside short and empty ones, with MTP (s_q = 2, count-based
+    causality).  Automatic splits run the device work plan; 4 and 64 uniform
+    splits run the per-token split path."""
     rng = np.random.default_rng(74)
-    pool, lens = 150_000, [140_000, 300]
-    q = oracle.normal_bf16(rng, (len(lens), H, D_QK))
+    pool, lens, s_q = 220_000, [200_000, 300, 2_100, 0], 2
+    B = len(lens)
+    q = oracle.normal_bf16(rng, (B * s_q, H, D_QK))
     kv = bf16_rows(rng, pool)
     indptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     indices = np.concatenate([rng.permutation(pool)[:n] for n in lens]).astype(np.int32)
     indices[5000:5100] = -1                  # skipped rows
-    print(f"[case] CSR decode list of {lens[0]} rows", flush=True)
-    # The oracle on the top-k form of the same lists, in 14 ranges of 10,000
-    # entries run side by side (one oracle task is one whole list), merged by
-    # the oracle's split combine.
-    idx = np.full((len(lens), 1, max(lens)), -1, np.int32)
+    print(f"[case] CSR decode lists {lens}, s_q={s_q}", flush=True)
+    # The oracle on the top-k form of the same lists (query token t of batch b
+    # sees the first len - (s_q - 1 - t) entries), in ranges of 10,000 entries
+    # run side by side (one oracle task is one whole list), merged by the
+    # oracle's split combine.
+    width = max(lens)
+    idx = np.full((B, s_q, width), -1, np.int32)
     for b, n in enumerate(lens):
-        idx[b, 0, :n] = indices[indptr[b]:indptr[b + 1]]
-    q4 = q.reshape(len(lens), 1, H, D_QK)
-    sl = np.full(len(lens), pool, np.int32)
+        for t in range(s_q):
+            m = max(0, n - (s_q - 1 - t))
+            idx[b, t, :m] = indices[indptr[b]:indptr[b] + m]
+    q4 = q.reshape(B, s_q, H, D_QK)
+    sl = np.full(B, pool, np.int32)
 
     def part(r0):
         sub = np.ascontiguousarray(idx[:, :, r0:r0 + 10_000])
         return oracle.mla_decode_partial(q4, kv, sub, sl, SM_SCALE, 0, sub.shape[2], num_threads=2)
 
     with ThreadPoolExecutor(8) as ex:
-        parts = list(ex.map(part, range(0, max(lens), 10_000)))
+        parts = list(ex.map(part, range(0, width, 10_000)))
     o_ref, l_ref = oracle.mla_combine(np.stack([p[0] for p in parts]), np.stack([p[1] for p in parts]))
     for ns in (0, 4, 64):
         out, lse = dsa.mla_decode_csr(t16(q, dev), t16(kv, dev), torch.from_numpy(indptr).to(dev),
-                                      torch.from_numpy(indices).to(dev), SM_SCALE, s_q=1,
+                                      torch.from_numpy(indices).to(dev), SM_SCALE, s_q=s_q,
                                       max_kv_len=max(lens), num_splits=ns)
         torch.cuda.synchronize()
-        e = assert_parity(bits(out), lse.cpu().numpy(), o_ref, l_ref, f"CSR long list splits={ns}")
+        e = assert_parity(bits(out), lse.cpu().numpy(), o_ref, l_ref, f"CSR skewed splits={ns}")
         print(f"[case] splits={ns}: max|dO|={e[0]:.3e} max rel dLSE={e[1]:.3e}", flush=True)
