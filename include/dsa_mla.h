@@ -62,6 +62,9 @@ extern "C" {
 #define DSA_MLA_FP8_ROW_BYTES 656
 #define DSA_MLA_BF16_ROW_BYTES 1152
 #define DSA_MLA_MAX_SPLITS 64
+/* num_splits of the CSR entries: the workspace already holds the work plan
+ * of these lists (dsa_mla_csr_plan) */
+#define DSA_MLA_SPLITS_PLANNED (-1)
 /* longest list an entry takes (top-k, max_kv_len, max_rows): INT32_MAX - 2048 */
 #define DSA_MLA_MAX_LIST 2147481599
 #define DSA_MLA_D_V4 512       /* V4 prefill head dim: K = V = a 512-value row */
@@ -221,6 +224,10 @@ int dsa_mla_combine(const float* partial_o, const float* partial_lse, int32_t nu
  *            directly, a longer row's items write partials that the combine
  *            merges.  The workspace then holds the plan and at most 512
  *            partial rows (H x 513 fp32 each), none when max_kv_len <= 128.
+ *            DSA_MLA_SPLITS_PLANNED (-1): as 0, with the plan already in the
+ *            workspace (dsa_mla_csr_plan, or an earlier call with 0, on the
+ *            same kv_indptr, B, s_q, H and max_kv_len): the plan is built once
+ *            and reused by every layer of a decode step.
  *            1..DSA_MLA_MAX_SPLITS: every row cut into num_splits equal
  *            parts (workspace: num_splits partial rows per row; none for 1).
  */
@@ -248,6 +255,18 @@ int dsa_mla_decode_csr_workspace_size(const dsa_mla_decode_csr_args* args, size_
 /* Launch the CSR decode (kernel + split combine) on `stream`. */
 int dsa_mla_decode_csr(const dsa_mla_decode_csr_args* args, void* workspace, size_t workspace_bytes,
                        void* stream);
+
+/*
+ * Build the CSR work plan of kv_indptr (B batches, s_q query tokens each,
+ * lists of at most max_kv_len entries, H heads) into `workspace` (at least
+ * dsa_mla_decode_csr_workspace_size / dsa_mla_decode_mxfp8_workspace_size
+ * bytes for num_splits 0), for later calls with num_splits =
+ * DSA_MLA_SPLITS_PLANNED.  The counterpart of get_mla_metadata_kernel,
+ * which the reference harness runs once before its timed loop
+ * (opus_attn/dsa_v32/common/host.cc:266-272).  Runs on `stream`.
+ */
+int dsa_mla_csr_plan(const int32_t* kv_indptr, int32_t B, int32_t s_q, int32_t H, int32_t max_kv_len,
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Sparse MLA decode on MXFP8 split streams, CSR form: the argument set of
@@ -437,7 +456,8 @@ int dsa_kv_quantize_fp8(const void* src_bf16, int64_t src_stride, int64_t n_rows
 /* Human-readable text for a DSA_ERR_* code. */
 const char* dsa_mla_strerror(int code);
 
-/* ABI version, bumped on any change of the argument structs. */
+/* ABI version, bumped on any change of the argument structs or of an
+ * argument's meaning. */
 int dsa_mla_abi_version(void);
 
 #ifdef __cplusplus

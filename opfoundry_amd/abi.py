@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(PKG_DIR, "_build", "libdsa_mla.so")
 D_QK, D_NOPE, D_ROPE, D_VO = 576, 512, 64, 512
 FP8_ROW_BYTES, BF16_ROW_BYTES = 656, 1152
 MAX_SPLITS = 64
+SPLITS_PLANNED = -1               # DSA_MLA_SPLITS_PLANNED: CSR plan already in the workspace
 MAX_LIST = 2 ** 31 - 1 - 2048      # DSA_MLA_MAX_LIST: longest top-k / max_kv_len / max_rows
 
 KV_BF16 = 0
@@ -47,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "dsa_mla_decode_noalloc",
     "dsa_mla_decode_csr_workspace_size",
     "dsa_mla_decode_csr",
+    "dsa_mla_csr_plan",
     "dsa_mla_decode_mxfp8_workspace_size",
     "dsa_mla_decode_mxfp8",
     "dsa_mla_combine",
@@ -60,7 +62,7 @@ EXPORTED_SYMBOLS = (
     "dsa_mla_abi_version",
 )
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -190,6 +192,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.dsa_mla_decode_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     lib.dsa_mla_decode_csr_workspace_size.argtypes = [ctypes.POINTER(CsrArgs), sz]
     lib.dsa_mla_decode_csr.argtypes = [ctypes.POINTER(CsrArgs), _vp, ctypes.c_size_t, _vp]
+    lib.dsa_mla_csr_plan.argtypes = [_vp, _i32, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp]
     lib.dsa_mla_decode_mxfp8_workspace_size.argtypes = [ctypes.POINTER(MxArgs), sz]
     lib.dsa_mla_decode_mxfp8.argtypes = [ctypes.POINTER(MxArgs), _vp, ctypes.c_size_t, _vp]
     lib.dsa_mla_combine.argtypes = [_vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _vp]

@@ -1299,15 +1299,16 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 // grid = (rows, ceil(H / 4)), block = 256.
 // ---------------------------------------------------------------------------
 // ---------------------------------------------------------------------------
-// CSR work plan: one workgroup of 1024 threads, on the device (the host cannot
+// CSR work plan: one workgroup of 256 threads, on the device (the host cannot
 // read the lists).  Query row q = b * s_q + t attends
 // L_q = kv_indptr[b+1] - kv_indptr[b] - (s_q - 1 - t) entries (count-based
 // MTP causality).  The plan cuts the lists into work items of at most
-// `chunk` entries, chunk = max(PLAN_MIN_CHUNK, total / (PLAN_TARGET - rows))
-// (total / PLAN_TARGET from PLAN_TARGET rows on) rounded up to a tile, so
-// that the items of all rows together fill about PLAN_TARGET workgroups,
-// in one round when there are fewer rows, however the lengths are spread:
-// a long list spreads over many workgroups, a short one stays whole.  A row no longer than chunk
+// `chunk` entries (a multiple of the tile, >= PLAN_MIN_CHUNK): below
+// PLAN_TARGET rows the smallest chunk whose items fit one round of
+// PLAN_TARGET workgroups, from PLAN_TARGET rows on total / PLAN_TARGET (a row
+// longer than that splits, an average one does not).  However the lengths
+// are spread, a long list spreads over many workgroups and a short one stays
+// whole.  A row no longer than chunk
 // is one item that writes its output directly; a longer row's items write
 // consecutive partial rows, listed in `splits` for the combine.  Bounds:
 // items <= rows + PLAN_TARGET, split rows < PLAN_TARGET, partial rows
@@ -1320,7 +1321,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 // ---------------------------------------------------------------------------
 constexpr int PLAN_TARGET = 256;     // workgroups a plan aims at: one per CU
 constexpr int PLAN_MIN_CHUNK = 128;  // entries: at least four tiles per item
-constexpr int PLAN_THREADS = 1024;
+constexpr int PLAN_THREADS = 256;
 
 __global__ void __launch_bounds__(PLAN_THREADS)
 dsa_csr_plan_kernel(const int32_t* __restrict__ indptr, int B, int s_q, int max_len, int4* __restrict__ items,
@@ -1336,21 +1337,52 @@ dsa_csr_plan_kernel(const int32_t* __restrict__ indptr, int B, int s_q, int max_
         const int64_t L = (int64_t)indptr[b + 1] - indptr[b] - (s_q - 1 - t);
         return L > max_len ? -1 : (int)max(L, (int64_t)0);
     };
-    long long tot = 0;
-    for (int q = tid; q < rows; q += PLAN_THREADS) tot += max(len_of(q), 0);
+    static_assert(PLAN_TARGET <= PLAN_THREADS, "below PLAN_TARGET rows, one row per thread");
+    const bool few = rows < PLAN_TARGET;
+    const int Lr = few && tid < rows ? len_of(tid) : 0;    // this thread's row when few
+    int chunk;
+    if (!few) {
+        long long tot = 0;
+        for (int q = tid; q < rows; q += PLAN_THREADS) tot += max(len_of(q), 0);
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) tot += __shfl_xor(tot, off, 64);
-    if (lane == 0) s_tot[wave] = tot;
-    __syncthreads();
-    long long total = 0;
-    for (int w = 0; w < NW; ++w) total += s_tot[w];
-    // Fewer rows than PLAN_TARGET: every row's last item may be partly empty,
-    // so chunk >= total / (PLAN_TARGET - rows) keeps all items in one round of
-    // PLAN_TARGET workgroups (items <= total / chunk + rows).
-    const long long slots = rows < PLAN_TARGET ? PLAN_TARGET - rows : PLAN_TARGET;
-    long long c64 = max((long long)PLAN_MIN_CHUNK, (total + slots - 1) / slots);
-    c64 = (c64 + TILE - 1) / TILE * TILE;
-    const int chunk = (int)min(c64, (long long)MAX_LIST);
+        for (int off = 32; off >= 1; off >>= 1) tot += __shfl_xor(tot, off, 64);
+        if (lane == 0) s_tot[wave] = tot;
+        __syncthreads();
+        long long total = 0;
+        for (int w = 0; w < NW; ++w) total += s_tot[w];
+        long long c64 = max((long long)PLAN_MIN_CHUNK, (total + PLAN_TARGET - 1) / PLAN_TARGET);
+        c64 = (c64 + TILE - 1) / TILE * TILE;
+        chunk = (int)min(c64, (long long)MAX_LIST);
+    } else {
+        // Fewer rows than PLAN_TARGET (one per thread): the smallest chunk, in
+        // tiles and >= PLAN_MIN_CHUNK, whose items fit one round of
+        // PLAN_TARGET workgroups, sum over rows of ceil(L / chunk) <=
+        // PLAN_TARGET (a cut row is one item).  The count falls as chunk
+        // grows, and chunk = the longest list gives rows items: bisection.
+        __shared__ int s_cnt[NW];
+        int lmax = Lr;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) lmax = max(lmax, __shfl_xor(lmax, off, 64));
+        if (lane == 0) s_cnt[wave] = lmax;
+        __syncthreads();
+        for (int w = 0; w < NW; ++w) lmax = max(lmax, s_cnt[w]);
+        __syncthreads();
+        int lo = PLAN_MIN_CHUNK / TILE, hi = max(lo, (lmax + TILE - 1) / TILE);   // in tiles
+        while (lo < hi) {
+            const int mid = (lo + hi) / 2, c = mid * TILE;
+            int n = tid < rows ? (Lr <= c ? 1 : (Lr + c - 1) / c) : 0;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) n += __shfl_xor(n, off, 64);
+            if (lane == 0) s_cnt[wave] = n;
+            __syncthreads();
+            int cnt = 0;
+            for (int w = 0; w < NW; ++w) cnt += s_cnt[w];
+            __syncthreads();
+            if (cnt <= PLAN_TARGET) hi = mid;
+            else lo = mid + 1;
+        }
+        chunk = lo * TILE;
+    }
     auto wave_incl = [&](int v) {
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
@@ -1364,7 +1396,7 @@ dsa_csr_plan_kernel(const int32_t* __restrict__ indptr, int B, int s_q, int max_
         const int q = q0 + tid;
         int L = 0, n = 0;
         if (q < rows) {
-            L = len_of(q);
+            L = few ? Lr : len_of(q);
             n = L <= chunk ? 1 : (L + chunk - 1) / chunk;
         }
         const int ns = n > 1 ? n : 0, sp = n > 1 ? 1 : 0;
@@ -1402,27 +1434,12 @@ dsa_csr_plan_kernel(const int32_t* __restrict__ indptr, int B, int s_q, int max_
     }
 }
 
-__global__ void __launch_bounds__(256)
-dsa_mla_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_lse, int ns,
-                       int rows, int H, int s_q, __bf16* __restrict__ out, int64_t o_sb, int64_t o_st,
-                       int64_t o_sh, float* __restrict__ lse, const int4* __restrict__ map,
-                       const int32_t* __restrict__ hdr) {
-    int row = blockIdx.x;
-    const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (head >= H) return;
-    // uniform splits: split s of row r is partial row s * rows + r.  A CSR
-    // plan lists its split query rows instead: (query row, first partial
-    // row, count) with consecutive partial rows; hdr[1] rows are listed.
-    int64_t first = row, step_rows = rows;
-    if (map) {
-        if (row >= hdr[1]) return;
-        const int4 m = map[row];
-        row = m.x;
-        first = m.y;
-        ns = m.z;
-        step_rows = 1;
-    }
+// One (query row, head) of a combine, on one wave: ns partial rows, split s
+// at partial row first + s * step_rows.
+__device__ __forceinline__ void combine_head(const float* __restrict__ part_o, const float* __restrict__ part_lse,
+                                             int ns, int64_t first, int64_t step_rows, int row, int head, int H,
+                                             int s_q, __bf16* __restrict__ out, int64_t o_sb, int64_t o_st,
+                                             int64_t o_sh, float* __restrict__ lse, int lane) {
     const int64_t stride = step_rows * H;
     const int64_t base = first * H + head;     // partial index of split 0
     const int64_t rh = (int64_t)row * H + head;
@@ -1465,6 +1482,42 @@ dsa_mla_combine_kernel(const float* __restrict__ part_o, const float* __restrict
     reinterpret_cast<u32x2*>(op)[0] = __builtin_bit_cast(u32x2, b0);
     reinterpret_cast<u32x2*>(op)[1] = __builtin_bit_cast(u32x2, b1);
     if (lse && lane == 0) lse[rh] = den > 0.0f || den != den ? m + __builtin_amdgcn_logf(den) * LN2 : INFINITY;
+}
+
+// uniform splits: split s of row r is partial row s * rows + r.
+// grid = (rows, ceil(H / 4)), block = 256: one wave per (row, head).
+__global__ void __launch_bounds__(256)
+dsa_mla_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_lse, int ns,
+                       int rows, int H, int s_q, __bf16* __restrict__ out, int64_t o_sb, int64_t o_st,
+                       int64_t o_sh, float* __restrict__ lse) {
+    const int row = blockIdx.x;
+    const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (head >= H) return;
+    combine_head(part_o, part_lse, ns, row, rows, row, head, H, s_q, out, o_sb, o_st, o_sh, lse,
+                 threadIdx.x & 63);
+}
+
+// The split rows of a CSR work plan: map[i] = (query row, first partial row,
+// count), consecutive partial rows, hdr[1] rows listed.  A fixed grid walks
+// the hdr[1] x ceil(H / 4) units of four heads, so a plan without split rows
+// costs one wave of empty workgroups, not a workgroup per possible unit.
+__global__ void __launch_bounds__(256)
+dsa_mla_combine_plan_kernel(const float* __restrict__ part_o, const float* __restrict__ part_lse, int H,
+                            int s_q, __bf16* __restrict__ out, int64_t o_sb, int64_t o_st, int64_t o_sh,
+                            float* __restrict__ lse, const int4* __restrict__ map,
+                            const int32_t* __restrict__ hdr) {
+    const int hq = (H + 3) / 4;
+    const int units = __builtin_amdgcn_readfirstlane(hdr[1]) * hq;
+    const int wave = threadIdx.x >> 6;
+    for (int u = blockIdx.x; u < units; u += gridDim.x) {
+        const int r = u / hq;
+        const int head = (u - r * hq) * 4 + wave;
+        if (head < H) {
+            const int4 m = map[r];
+            combine_head(part_o, part_lse, m.z, m.y, 1, m.x, head, H, s_q, out, o_sb, o_st, o_sh, lse,
+                         threadIdx.x & 63);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1642,7 +1695,7 @@ int launch_combine(const float* po, const float* pl, int ns, int rows, int H, in
     if (rows == 0) return DSA_OK;
     dim3 grid(rows, (H + 3) / 4), block(256);
     hipLaunchKernelGGL(dsa_mla_combine_kernel, grid, block, 0, st, po, pl, ns, rows, H, s_q, (__bf16*)out, o_sb,
-                       o_st, o_sh, lse, (const int4*)nullptr, (const int32_t*)nullptr);
+                       o_st, o_sh, lse);
     return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_HIP;
 }
 
@@ -1672,16 +1725,26 @@ CsrPlanLayout csr_plan_layout(int B, int s_q, int H, int max_len) {
 bool plan_grid_ok(int B, int s_q, int H) {
     return ((int64_t)B * s_q + PLAN_TARGET) * head_groups(H) <= INT32_MAX - PLAN_THREADS;
 }
-// plan kernel, forward kernel over the plan's items, combine of the split rows
-int csr_plan_launch(FwdParams& fp, int fmt, int max_len, void* ws, hipStream_t st) {
+// the plan kernel alone (into a workspace laid out by csr_plan_layout)
+int csr_plan_build(const int32_t* kv_indptr, int B, int s_q, int H, int max_len, void* ws, hipStream_t st) {
+    const CsrPlanLayout L = csr_plan_layout(B, s_q, H, max_len);
+    char* w = (char*)ws;
+    hipLaunchKernelGGL(dsa_csr_plan_kernel, dim3(1), dim3(PLAN_THREADS), 0, st, kv_indptr, B, s_q, max_len,
+                       (int4*)(w + L.items), (int4*)(w + L.map), (int32_t*)w);
+    return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_HIP;
+}
+// (plan kernel,) forward kernel over the plan's items, combine of the split rows;
+// build = false: the workspace already holds the plan of these lists
+int csr_plan_launch(FwdParams& fp, int fmt, int max_len, void* ws, bool build, hipStream_t st) {
     const CsrPlanLayout L = csr_plan_layout(fp.B, fp.s_q, fp.H, max_len);
     char* w = (char*)ws;
     int32_t* hdr = (int32_t*)w;
     int4* items = (int4*)(w + L.items);
     int4* map = (int4*)(w + L.map);
-    hipLaunchKernelGGL(dsa_csr_plan_kernel, dim3(1), dim3(PLAN_THREADS), 0, st, fp.kv_indptr, fp.B, fp.s_q, max_len,
-                       items, map, hdr);
-    if (hipGetLastError() != hipSuccess) return DSA_ERR_HIP;
+    if (build) {
+        const int r = csr_plan_build(fp.kv_indptr, fp.B, fp.s_q, fp.H, max_len, ws, st);
+        if (r) return r;
+    }
     fp.plan_items = items;
     fp.plan_hdr = hdr;
     fp.chunk = max_len;      // one launch "split": lists longer than max_len are cut
@@ -1691,10 +1754,9 @@ int csr_plan_launch(FwdParams& fp, int fmt, int max_len, void* ws, hipStream_t s
     }
     const int r = launch_fwd(fp, fmt, L.items_max, 1, 1, st);
     if (r || !L.slots_max) return r;
-    dim3 grid(PLAN_TARGET, (fp.H + 3) / 4), block(256);
-    hipLaunchKernelGGL(dsa_mla_combine_kernel, grid, block, 0, st, (const float*)fp.part_o, (const float*)fp.part_lse,
-                       0, 0, fp.H, fp.s_q, fp.out, fp.o_sb, fp.o_st, fp.o_sh, fp.lse, (const int4*)map,
-                       (const int32_t*)hdr);
+    hipLaunchKernelGGL(dsa_mla_combine_plan_kernel, dim3(4 * PLAN_TARGET), dim3(256), 0, st, (const float*)fp.part_o,
+                       (const float*)fp.part_lse, fp.H, fp.s_q, fp.out, fp.o_sb, fp.o_st, fp.o_sh, fp.lse,
+                       (const int4*)map, (const int32_t*)hdr);
     return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_HIP;
 }
 
@@ -1705,11 +1767,12 @@ int validate_csr(const dsa_mla_decode_csr_args* a, int* ns_out, int* chunk_out) 
     if (!heads_ok(a->H, a->B)) return DSA_ERR_BAD_SHAPE;
     if (a->kv_format != DSA_KV_BF16 && a->kv_format != DSA_KV_FP8_656) return DSA_ERR_BAD_FORMAT;
     if (row_stride_bytes(a->kv_format, a->stride_kv_page) < 0) return DSA_ERR_BAD_STRIDE;
-    if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
-    // num_splits 0: the device work plan (ns 0 below); else uniform splits
+    if (a->num_splits < DSA_MLA_SPLITS_PLANNED || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
+    // num_splits 0: build the device work plan; DSA_MLA_SPLITS_PLANNED: the
+    // workspace holds it (dsa_mla_csr_plan); else uniform splits
     const int ns = a->num_splits;
-    if (ns == 0 && !plan_grid_ok(a->B, a->s_q, a->H)) return DSA_ERR_BAD_SHAPE;
-    const int chunk = a->max_kv_len == 0 || ns == 0 ? a->max_kv_len : (a->max_kv_len + ns - 1) / ns;
+    if (ns <= 0 && !plan_grid_ok(a->B, a->s_q, a->H)) return DSA_ERR_BAD_SHAPE;
+    const int chunk = a->max_kv_len == 0 || ns <= 0 ? a->max_kv_len : (a->max_kv_len + ns - 1) / ns;
     if (a->B > 0) {
         // the kernel reads Q even when every list is empty
         if (!a->out || !a->kv_indptr || !a->q) return DSA_ERR_NULL_POINTER;
@@ -1727,7 +1790,7 @@ int validate_csr(const dsa_mla_decode_csr_args* a, int* ns_out, int* chunk_out) 
 }
 size_t csr_ws_bytes(const dsa_mla_decode_csr_args* a, int ns) {
     if (a->B == 0) return 0;
-    if (ns == 0) return csr_plan_layout(a->B, a->s_q, a->H, a->max_kv_len).total;
+    if (ns <= 0) return csr_plan_layout(a->B, a->s_q, a->H, a->max_kv_len).total;
     return ns == 1 ? 0 : (size_t)ns * a->B * a->s_q * a->H * (D_VO + 1) * sizeof(float) + 256;
 }
 
@@ -1736,11 +1799,12 @@ int validate_mx(const dsa_mla_decode_mxfp8_args* a, int* ns_out, int* chunk_out)
     if (a->B < 0 || a->s_q <= 0 || a->max_kv_len < 0 || a->max_kv_len > MAX_LIST || a->total_tokens < 0)
         return DSA_ERR_BAD_SHAPE;
     if (!heads_ok(a->H, a->B)) return DSA_ERR_BAD_SHAPE;
-    if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
-    // num_splits 0: the device work plan (ns 0 below); else uniform splits
+    if (a->num_splits < DSA_MLA_SPLITS_PLANNED || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
+    // num_splits 0: build the device work plan; DSA_MLA_SPLITS_PLANNED: the
+    // workspace holds it (dsa_mla_csr_plan); else uniform splits
     const int ns = a->num_splits;
-    if (ns == 0 && !plan_grid_ok(a->B, a->s_q, a->H)) return DSA_ERR_BAD_SHAPE;
-    const int chunk = a->max_kv_len == 0 || ns == 0 ? a->max_kv_len : (a->max_kv_len + ns - 1) / ns;
+    if (ns <= 0 && !plan_grid_ok(a->B, a->s_q, a->H)) return DSA_ERR_BAD_SHAPE;
+    const int chunk = a->max_kv_len == 0 || ns <= 0 ? a->max_kv_len : (a->max_kv_len + ns - 1) / ns;
     if (a->B > 0) {
         // the kernel reads Q even when every list is empty
         if (!a->out || !a->kv_indptr || !a->q_nope || !a->q_scale || !a->q_rope) return DSA_ERR_NULL_POINTER;
@@ -1764,7 +1828,7 @@ int validate_mx(const dsa_mla_decode_mxfp8_args* a, int* ns_out, int* chunk_out)
 }
 size_t mx_ws_bytes(const dsa_mla_decode_mxfp8_args* a, int ns) {
     if (a->B == 0) return 0;
-    if (ns == 0) return csr_plan_layout(a->B, a->s_q, a->H, a->max_kv_len).total;
+    if (ns <= 0) return csr_plan_layout(a->B, a->s_q, a->H, a->max_kv_len).total;
     return ns == 1 ? 0 : (size_t)ns * a->B * a->s_q * a->H * (D_VO + 1) * sizeof(float) + 256;
 }
 
@@ -1772,7 +1836,7 @@ size_t mx_ws_bytes(const dsa_mla_decode_mxfp8_args* a, int ns) {
 
 extern "C" {
 
-int dsa_mla_abi_version(void) { return 6; }
+int dsa_mla_abi_version(void) { return 7; }
 
 const char* dsa_mla_strerror(int code) {
     switch (code) {
@@ -1879,6 +1943,17 @@ int decode_launch(const dsa_mla_decode_args* a, int ns, int chunk, void* ws, hip
 
 extern "C" {
 
+int dsa_mla_csr_plan(const int32_t* kv_indptr, int32_t B, int32_t s_q, int32_t H, int32_t max_kv_len, void* ws,
+                     size_t ws_bytes, void* stream) {
+    if (B < 0 || s_q <= 0 || max_kv_len < 0 || max_kv_len > MAX_LIST) return DSA_ERR_BAD_SHAPE;
+    if (!heads_ok(H, B) || !plan_grid_ok(B, s_q, H)) return DSA_ERR_BAD_SHAPE;
+    if (B == 0) return DSA_OK;
+    if (!kv_indptr) return DSA_ERR_NULL_POINTER;
+    const size_t need = csr_plan_layout(B, s_q, H, max_kv_len).total;
+    if (!ws || ws_bytes < need || ((uintptr_t)ws & 15)) return DSA_ERR_WORKSPACE;
+    return csr_plan_build(kv_indptr, B, s_q, H, max_kv_len, ws, (hipStream_t)stream);
+}
+
 int dsa_mla_decode_csr_workspace_size(const dsa_mla_decode_csr_args* a, size_t* bytes) {
     if (!bytes) return DSA_ERR_NULL_POINTER;
     int ns, chunk;
@@ -1912,7 +1987,7 @@ int dsa_mla_decode_csr(const dsa_mla_decode_csr_args* a, void* ws, size_t ws_byt
     fp.lse = a->lse;
     fp.B = a->B; fp.s_q = a->s_q; fp.topk = a->max_kv_len; fp.chunk = chunk;
     fp.scale_log2 = a->softmax_scale * LOG2E;
-    if (ns == 0) return csr_plan_launch(fp, a->kv_format, a->max_kv_len, ws, st);
+    if (ns <= 0) return csr_plan_launch(fp, a->kv_format, a->max_kv_len, ws, ns == 0, st);
     if (ns > 1) {
         const size_t rows = (size_t)a->B * a->s_q * a->H;
         fp.part_o = (float*)ws;
@@ -1965,7 +2040,7 @@ int dsa_mla_decode_mxfp8(const dsa_mla_decode_mxfp8_args* a, void* ws, size_t ws
     fp.lse = a->lse;
     fp.B = a->B; fp.s_q = a->s_q; fp.topk = a->max_kv_len; fp.chunk = chunk;
     fp.scale_log2 = a->softmax_scale * LOG2E;
-    if (ns == 0) return csr_plan_launch(fp, DSA_KV_MXFP8, a->max_kv_len, ws, st);
+    if (ns <= 0) return csr_plan_launch(fp, DSA_KV_MXFP8, a->max_kv_len, ws, ns == 0, st);
     if (ns > 1) {
         const size_t rows = (size_t)a->B * a->s_q * a->H;
         fp.part_o = (float*)ws;

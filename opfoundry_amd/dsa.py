@@ -203,6 +203,29 @@ def mla_decode_csr(q: torch.Tensor, kv: torch.Tensor, kv_indptr: torch.Tensor,
     return out, lse
 
 
+def csr_plan(kv_indptr: torch.Tensor, B: int, s_q: int, H: int, max_kv_len: int,
+             workspace: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Build the CSR work plan of kv_indptr into a workspace (allocated when None) and return
+    it; decode calls with num_splits=abi.SPLITS_PLANNED and that workspace reuse the plan
+    (dsa_mla_csr_plan)."""
+    _need(kv_indptr, torch.int32, "kv_indptr")
+    lib = load_library()
+    a = abi.CsrArgs()
+    a.B, a.s_q, a.H, a.max_kv_len, a.num_splits = B, s_q, H, max_kv_len, 0
+    a.q = a.kv = a.out = a.kv_indptr = a.kv_indices = 16        # sizing only: any aligned non-null
+    a.stride_q_b, a.stride_q_h, a.stride_o_b, a.stride_o_h = H * 576, 576, H * 512, 512
+    a.kv_format = abi.KV_BF16
+    n = ctypes.c_size_t(0)
+    check(lib.dsa_mla_decode_csr_workspace_size(ctypes.byref(a), ctypes.byref(n)),
+          "dsa_mla_decode_csr_workspace_size")
+    if workspace is None or workspace.numel() * workspace.element_size() < n.value:
+        workspace = torch.empty(max(n.value, 16), dtype=torch.uint8, device=kv_indptr.device)
+    check(lib.dsa_mla_csr_plan(_ptr(kv_indptr), B, s_q, H, max_kv_len, _ptr(workspace),
+                               workspace.numel() * workspace.element_size(), _stream(stream)),
+          "dsa_mla_csr_plan")
+    return workspace
+
+
 def make_decode_mxfp8_args(q_nope, q_scale, q_rope, kv_nope, kv_scale, kv_rope, kv_indptr,
                            kv_indices, sm_scale, out, lse, *, s_q=1, max_kv_len=None, num_splits=0):
     """dsa_mla_decode_mxfp8_args for split-stream tensors: q_nope uint8 [T, H, 512], q_scale

@@ -501,3 +501,21 @@ def test_head_groups_bound_the_grid(lib):
     2^31 - 1 the call is a bad shape."""
     assert _ws(lib, _decode_args(H=1 << 20, B=1 << 24, num_splits=1))[0] == -2
     assert _ws(lib, _decode_args(H=1 << 7, B=1 << 24, num_splits=1))[0] == 0
+
+
+def test_csr_plan_entry_validates(lib):
+    """dsa_mla_csr_plan checks its shape, pointers and workspace before any launch;
+    num_splits = DSA_MLA_SPLITS_PLANNED sizes the same workspace as num_splits = 0."""
+    ws0 = _csr_ws(lib, _csr_args(num_splits=0))
+    assert ws0[0] == 0 and _csr_ws(lib, _csr_args(num_splits=abi.SPLITS_PLANNED)) == ws0
+    assert _csr_ws(lib, _csr_args(num_splits=-2))[0] == -6
+    f = lib.dsa_mla_csr_plan
+    assert f(None, 0, 1, 128, 100, None, 0, None) == 0                    # empty batch: a no-op
+    assert f(None, 4, 2, 128, 3000, ctypes.c_void_p(0x10000), ws0[1], None) == -1
+    assert f(ctypes.c_void_p(0x5000), 4, 2, 128, 3000, None, 0, None) == -5
+    assert f(ctypes.c_void_p(0x5000), 4, 2, 128, 3000, ctypes.c_void_p(0x10000), ws0[1] - 1, None) == -5
+    assert f(ctypes.c_void_p(0x5000), 4, 2, 128, 3000, ctypes.c_void_p(0x10008), ws0[1], None) == -5
+    assert f(ctypes.c_void_p(0x5000), -1, 2, 128, 3000, None, 0, None) == -2
+    assert f(ctypes.c_void_p(0x5000), 4, 0, 128, 3000, None, 0, None) == -2
+    assert f(ctypes.c_void_p(0x5000), 4, 2, 0, 3000, None, 0, None) == -2
+    assert f(ctypes.c_void_p(0x5000), 4, 2, 128, abi.MAX_LIST + 1, None, 0, None) == -2

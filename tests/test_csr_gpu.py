@@ -23,7 +23,7 @@ import torch
 
 import oracle
 from _cases import D_QK, SM_SCALE, assert_parity, bf16_rows, fp8_rows
-from opfoundry_amd import dsa
+from opfoundry_amd import abi, dsa
 
 pytestmark = pytest.mark.gpu
 H = 128
@@ -177,8 +177,8 @@ def test_csr_list_longer_than_bound_is_nan(dev, ns):
 def test_csr_plan_invariants(dev):
     """The device work plan of an automatic-split CSR call, read back from the workspace
     (header at 0, item table at 256, split-row map after it, 256-byte aligned):
-    - chunk = max(128, ceil(total entries / (256 - rows))) rounded up to 32 (fewer than
-      256 rows), and at most 256 items;
+    - with fewer than 256 rows, chunk is the smallest multiple of 32 (>= 128) whose
+      items number at most 256;
     - each row's items are consecutive and cover [0, L) in chunk-sized pieces
       (one empty item for an empty row);
     - a row no longer than chunk writes directly (slot -1); a longer row's items use
@@ -202,10 +202,13 @@ def test_csr_plan_invariants(dev):
     hdr = w[:12].view(np.int32)
     n_items, n_split, chunk = (int(x) for x in hdr)
     L = [max(0, lens[q_ // s_q] - (s_q - 1 - q_ % s_q)) for q_ in range(rows)]
-    total = sum(L)
-    want = max(128, -(-total // (256 - rows)))
-    assert chunk == -(-want // 32) * 32
-    assert n_items <= 256
+    # fewer than 256 rows: the smallest chunk (in tiles, >= 128) whose items fit 256
+    def n_of(c):
+        return sum(1 if x <= c else -(-x // c) for x in L)
+    want = 128
+    while n_of(want) > 256:
+        want += 32
+    assert chunk == want and n_items == n_of(chunk) <= 256
     items = w[256:256 + 16 * n_items].view(np.int32).reshape(n_items, 4)
     items_max = rows + 256
     map_off = (256 + 16 * items_max + 255) // 256 * 256
@@ -227,3 +230,25 @@ def test_csr_plan_invariants(dev):
     assert pos == n_items
     assert [tuple(x[:3]) for x in smap] == split_rows
     assert len(split_rows) < 256 and len(slots) < 512 and sorted(slots) == list(range(len(slots)))
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_csr_plan_reuse(dev, fp8):
+    """A plan built once (dsa_mla_csr_plan) serves later calls with num_splits =
+    DSA_MLA_SPLITS_PLANNED on other queries over the same lists, bit-equal to calls
+    that build their own plan."""
+    lens, s_q = [5_000, 17, 0, 1_200], 2
+    q, kv, indptr, indices = csr_case(93 + fp8, lens, s_q, 8_000, fp8=fp8)
+    q2 = oracle.normal_bf16(np.random.default_rng(7), q.shape)
+    kvt = torch.from_numpy(kv).to(dev) if fp8 else t16(kv, dev)
+    ip, ix = torch.from_numpy(indptr).to(dev), torch.from_numpy(indices).to(dev)
+    ws = dsa.csr_plan(ip, len(lens), s_q, 128, max(lens))
+    for qq in (q, q2):
+        o_own, l_own = dsa.mla_decode_csr(t16(qq, dev), kvt, ip, ix, SM_SCALE, s_q=s_q)
+        o_pl, l_pl = dsa.mla_decode_csr(t16(qq, dev), kvt, ip, ix, SM_SCALE, s_q=s_q,
+                                        num_splits=abi.SPLITS_PLANNED, workspace=ws)
+        torch.cuda.synchronize()
+        assert (bits(o_pl) == bits(o_own)).all()
+        assert np.array_equal(l_pl.cpu().numpy(), l_own.cpu().numpy())
+    o_ref, l_ref = oracle_csr(q2, kv, indptr, indices, s_q)
+    assert_parity(bits(o_pl), l_pl.cpu().numpy(), o_ref, l_ref, "csr planned")
