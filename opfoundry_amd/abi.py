@@ -58,6 +58,7 @@ EXPORTED_SYMBOLS = (
     "dsa_mla_prefill_v4_fp8",
     "dsa_kv_quantize_fp8",
     "dsa_topk_indices",
+    "dsa_indexer_scores",
     "dsa_mla_strerror",
     "dsa_mla_abi_version",
 )
@@ -165,6 +166,21 @@ class PrefillV4Fp8Args(ctypes.Structure):
     ]
 
 
+class IndexerArgs(ctypes.Structure):
+    """dsa_indexer_args (include/dsa_indexer.h)."""
+
+    _fields_ = [
+        ("q", _vp), ("q_stride_b", _i64), ("q_stride_t", _i64), ("q_stride_h", _i64),
+        ("weights", _vp),
+        ("k_cache", _vp), ("k_total_rows", _i64), ("k_stride_row", _i64),
+        ("block_table", _vp), ("block_table_stride", _i64), ("block_size", _i32),
+        ("k_batch_stride", _i64),
+        ("seq_lens", _vp),
+        ("scores", _vp), ("score_stride", _i64),
+        ("B", _i32), ("s_q", _i32), ("H_I", _i32), ("n_cols", _i32), ("causal", _i32),
+    ]
+
+
 class DsaError(RuntimeError):
     def __init__(self, code: int, where: str):
         self.code = code
@@ -193,6 +209,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.dsa_mla_decode_csr_workspace_size.argtypes = [ctypes.POINTER(CsrArgs), sz]
     lib.dsa_mla_decode_csr.argtypes = [ctypes.POINTER(CsrArgs), _vp, ctypes.c_size_t, _vp]
     lib.dsa_mla_csr_plan.argtypes = [_vp, _i32, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp]
+    lib.dsa_indexer_scores.argtypes = [ctypes.POINTER(IndexerArgs), _vp]
     lib.dsa_mla_decode_mxfp8_workspace_size.argtypes = [ctypes.POINTER(MxArgs), sz]
     lib.dsa_mla_decode_mxfp8.argtypes = [ctypes.POINTER(MxArgs), _vp, ctypes.c_size_t, _vp]
     lib.dsa_mla_combine.argtypes = [_vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _vp]

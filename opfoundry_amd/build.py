@@ -15,7 +15,7 @@ import sys
 from .abi import LIB_PATH, PKG_DIR
 
 SRC = os.path.join(PKG_DIR, "csrc", "dsa_mla.hip")
-SRCS = [SRC, os.path.join(PKG_DIR, "csrc", "dsa_topk.hip")]
+SRCS = [SRC, os.path.join(PKG_DIR, "csrc", "dsa_topk.hip"), os.path.join(PKG_DIR, "csrc", "dsa_indexer.hip")]
 INCLUDE = os.path.normpath(os.path.join(PKG_DIR, "..", "include"))
 
 # Packed-fp32 VALU ops are disabled for all device code: only ordinary

@@ -527,3 +527,53 @@ def mla_prefill_v4_fp8(q_nope: torch.Tensor, q_rope: torch.Tensor, unified_kv_no
     a.softmax_scale = float(softmax_scale)
     check(load_library().dsa_mla_prefill_v4_fp8(ctypes.byref(a), _stream(stream)), "dsa_mla_prefill_v4_fp8")
     return out, lse
+
+
+def indexer_scores(q: torch.Tensor, weights: torch.Tensor, k_cache: torch.Tensor, seq_lens: torch.Tensor,
+                   *, block_table: Optional[torch.Tensor] = None, block_size: Optional[int] = None,
+                   causal: bool = False, n_cols: Optional[int] = None, k_batch_stride: int = 0,
+                   scores: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """DSA index scores (dsa_indexer_scores): q bf16 [B, s_q, H_I, 128], weights fp32
+    [B, s_q, H_I], k_cache bf16 [rows, 128] (or [blocks, block_size, 128]), seq_lens int32 [B].
+    Returns fp32 [B, s_q, n_cols]: score[b, t, j] = sum_h w * relu(q . k_j) for j < len(b, t)
+    (-inf where k_j's row lies outside the cache); other entries are left as allocated (NaN
+    here)."""
+    _need(q, torch.bfloat16, "q")
+    _need(weights, torch.float32, "weights")
+    _need(k_cache, torch.bfloat16, "k_cache")
+    _need(seq_lens, torch.int32, "seq_lens")
+    B, s_q, H_I, D = q.shape
+    if D != 128 or q.stride(3) != 1:
+        raise ValueError("q must be [B, s_q, H_I, 128] with a dense last dim")
+    if not weights.is_contiguous() or tuple(weights.shape) != (B, s_q, H_I):
+        raise ValueError("weights must be dense [B, s_q, H_I]")
+    kc = k_cache.reshape(-1, 128) if k_cache.is_contiguous() else k_cache
+    if kc.dim() != 2 or kc.shape[1] != 128 or kc.stride(1) != 1:
+        raise ValueError("k_cache must be [rows, 128] (or [blocks, block_size, 128]) with a dense last dim")
+    if n_cols is None:
+        n_cols = int(seq_lens.max().item()) if B else 0
+    if scores is None:
+        scores = torch.full((B, s_q, max(n_cols, 1)), float("nan"), dtype=torch.float32, device=q.device)
+    a = abi.IndexerArgs()
+    a.q = _ptr(q)
+    a.q_stride_b, a.q_stride_t, a.q_stride_h = q.stride(0), q.stride(1), q.stride(2)
+    a.weights = _ptr(weights)
+    a.k_cache = _ptr(kc)
+    a.k_total_rows = kc.shape[0]
+    a.k_stride_row = kc.stride(0)
+    if block_table is not None:
+        _need(block_table, torch.int32, "block_table")
+        if block_size is None:
+            block_size = k_cache.shape[-2] if k_cache.dim() >= 3 else None
+        if block_size is None:
+            raise ValueError("block_size is required with a block table")
+        a.block_table = _ptr(block_table)
+        a.block_table_stride = block_table.stride(0)
+        a.block_size = int(block_size)
+    a.k_batch_stride = int(k_batch_stride)
+    a.seq_lens = _ptr(seq_lens)
+    a.scores = _ptr(scores)
+    a.score_stride = scores.stride(1) if scores.dim() == 3 else scores.stride(0)
+    a.B, a.s_q, a.H_I, a.n_cols, a.causal = B, s_q, H_I, n_cols, 1 if causal else 0
+    check(load_library().dsa_indexer_scores(ctypes.byref(a), _stream(stream)), "dsa_indexer_scores")
+    return scores

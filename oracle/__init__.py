@@ -144,6 +144,37 @@ def topk_indices(scores: np.ndarray, lengths, topk: int) -> np.ndarray:
     return out
 
 
+def indexer_scores(q, weights, k_rows, seq_lens, *, block_table=None, block_size=1, k_batch_stride=0,
+                   causal=False, n_cols=None):
+    """The index scorer's contract (include/dsa_indexer.h; the reference has none - this is
+    the DeepSeek-V3.2 lightning indexer's score), in float64: q bf16 bits [B, s_q, H_I, 128],
+    weights f32 [B, s_q, H_I], k_rows bf16 bits [rows, 128].  Returns f64 [B, s_q, n_cols]:
+    score[b, t, j] = sum_h w[b, t, h] * max(0, q[b, t, h] . k[row(b, j)]) for
+    j < min(len(b, t), n_cols), -inf where the row lies outside the cache, NaN where no score
+    is defined (j past the list).  Rows as dsa_mla_decode's top-k form."""
+    qf = bf16_to_f32(np.asarray(q, np.uint16)).astype(np.float64)
+    kf = bf16_to_f32(np.asarray(k_rows, np.uint16).reshape(-1, 128)).astype(np.float64)
+    w = np.asarray(weights, np.float64)
+    B, s_q, H_I, _ = qf.shape
+    if n_cols is None:
+        n_cols = int(np.max(seq_lens)) if B else 0
+    out = np.full((B, s_q, n_cols), np.nan)
+    for b in range(B):
+        L = int(seq_lens[b])
+        for t in range(s_q):
+            n = min(max(L - (s_q - 1 - t) if causal else L, 0), n_cols)
+            j = np.arange(n)
+            if block_table is not None:
+                phys = block_table[b][j // block_size].astype(np.int64) * block_size + j % block_size
+            else:
+                phys = b * k_batch_stride + j
+            ok = (phys >= 0) & (phys < kf.shape[0])
+            dots = qf[b, t] @ kf[np.where(ok, phys, 0)].T          # [H_I, n]
+            s = (w[b, t][:, None] * np.maximum(dots, 0.0)).sum(0)
+            out[b, t, :n] = np.where(ok, s, -np.inf)
+    return out
+
+
 # ------------------------------------------------------------- attention
 
 def _decode_args(q, kv, fmt, indices, seq_lens, block_table, block_size, kv_batch_stride, causal,

@@ -57,7 +57,7 @@ def test_abi_version_and_strerror(lib):
 
 
 def _c_layout(struct: str, fields):
-    src = "#include <stddef.h>\n#include <stdio.h>\n#include \"dsa_mla.h\"\nint main(void){\n"
+    src = "#include <stddef.h>\n#include <stdio.h>\n#include \"dsa_mla.h\"\n#include \"dsa_indexer.h\"\nint main(void){\n"
     src += f'printf("%zu\\n", sizeof({struct}));\n'
     for f in fields:
         src += f'printf("%zu\\n", offsetof({struct}, {f}));\n'
@@ -75,6 +75,7 @@ def _c_layout(struct: str, fields):
 
 
 @pytest.mark.parametrize("cls,name", [(abi.DecodeArgs, "dsa_mla_decode_args"),
+                                      (abi.IndexerArgs, "dsa_indexer_args"),
                                       (abi.CsrArgs, "dsa_mla_decode_csr_args"),
                                       (abi.MxArgs, "dsa_mla_decode_mxfp8_args"),
                                       (abi.PrefillV4Fp8Args, "dsa_mla_prefill_v4_fp8_args"),
@@ -519,3 +520,34 @@ def test_csr_plan_entry_validates(lib):
     assert f(ctypes.c_void_p(0x5000), 4, 0, 128, 3000, None, 0, None) == -2
     assert f(ctypes.c_void_p(0x5000), 4, 2, 0, 3000, None, 0, None) == -2
     assert f(ctypes.c_void_p(0x5000), 4, 2, 128, abi.MAX_LIST + 1, None, 0, None) == -2
+
+
+def _ix_args(**kw):
+    a = abi.IndexerArgs()
+    a.q, a.weights, a.k_cache, a.seq_lens, a.scores = 0x1000, 0x2000, 0x3000, 0x4000, 0x5000
+    a.q_stride_b, a.q_stride_t, a.q_stride_h = 2 * 64 * 128, 64 * 128, 128
+    a.k_total_rows = 1 << 20
+    a.block_table, a.block_table_stride, a.block_size = 0x6000, 1024, 64
+    a.score_stride = 65536
+    a.B, a.s_q, a.H_I, a.n_cols, a.causal = 4, 2, 64, 65536, 1
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(B=-1), -2), (dict(s_q=0), -2), (dict(n_cols=-1), -2), (dict(k_total_rows=-1), -2),
+    (dict(H_I=48), -3), (dict(H_I=256), -3), (dict(block_size=0), -2),
+    (dict(k_stride_row=100), -7), (dict(k_stride_row=130), -7), (dict(score_stride=1000), -7),
+    (dict(q=None), -1), (dict(weights=None), -1), (dict(seq_lens=None), -1), (dict(scores=None), -1),
+    (dict(k_cache=None), -1), (dict(q_stride_h=100), -7), (dict(q=0x1008), -7), (dict(scores=0x5002), -7),
+])
+def test_indexer_rejects_bad_arguments(lib, kw, code):
+    assert lib.dsa_indexer_scores(ctypes.byref(_ix_args(**kw)), None) == code
+
+
+def test_indexer_empty_is_a_no_op(lib):
+    for kw in (dict(B=0), dict(n_cols=0), dict(B=0, q=None)):
+        assert lib.dsa_indexer_scores(ctypes.byref(_ix_args(**kw)), None) == 0
+    # no k rows at all: accepted (every position scores -inf), k_cache may be NULL
+    assert lib.dsa_indexer_scores(ctypes.byref(_ix_args(k_total_rows=0, k_cache=None, B=0)), None) == 0
