@@ -67,6 +67,9 @@ CONFIGS = {
     "topk": dict(kind="topk", T=256, n=65536, s_q=2, topk=2048, sets=5),
     # the reference harness's --varlen lists (host.cc:238-261): 8 batches, lengths U[5, 131072]
     "csr_skew": dict(kind="csr", B=8, s_q=1, s=131072),
+    # the index scorer in front of the c3 step's top-k: DeepSeek-V3.2 indexer shape (64 index
+    # heads of 128), B=128, MTP s_q=2, seq 65536 paged at 64, causal
+    "indexer": dict(kind="indexer", B=128, s_q=2, H_I=64, seq=65536, block=64),
 }
 NAMES = {
     "c1": "bf16 sparse MLA decode B=2 H=128 top-k 2048 (256 pad) flat KV 8192",
@@ -84,6 +87,8 @@ NAMES = {
              "causal lengths up to 65536, top-k 2048 (5 score sets alternate step by step)"),
     "csr_skew": ("bf16 CSR decode on the reference's --varlen lists: B=8, lengths U[5, 131072], "
                  "shuffled page table; device work plan against uniform splits"),
+    "indexer": ("DSA index scores (sum_h w * relu(q.k)), bf16 in / fp32 out: B=128, s_q=2 (MTP), 64 index "
+                "heads of 128, seq 65536 paged at 64, causal (the c3 step's score rows)"),
 }
 
 
@@ -799,6 +804,84 @@ def csr_skew_leg(args, dev):
     return leg
 
 
+def make_indexer(cfg, dev, seed=2081):
+    """Index-scorer inputs: q bf16 [B, s_q, H_I, 128] and k rows bf16 ~N(0, 1), weights
+    N(0, 1/H_I) fp32, the k cache paged at `block` rows through a shuffled block table."""
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    B, s_q, H_I, seq, bs = cfg["B"], cfg["s_q"], cfg["H_I"], cfg["seq"], cfg["block"]
+    mb = seq // bs
+    bt = torch.randperm(B * mb, generator=g, device=dev).to(torch.int32).view(B, mb)
+    k = torch.randn((B * mb * bs, 128), generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn((B, s_q, H_I, 128), generator=g, device=dev).to(torch.bfloat16)
+    w = torch.randn((B, s_q, H_I), generator=g, device=dev) / math.sqrt(H_I)
+    sl = torch.full((B,), seq, dtype=torch.int32, device=dev)
+    scores = torch.empty((B, s_q, seq), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    return dict(q=q, w=w, k=k, bt=bt, sl=sl, scores=scores, bs=bs, seq=seq)
+
+
+def indexer_leg(args, dev):
+    """The index scorer on the c3 step's shape: step time, HBM roofline (k rows read once per
+    sequence, scores written), MFMA share, and numpy's float64 oracle on a sample."""
+    import ctypes
+    import numpy as np
+    import torch
+    from opfoundry_amd import abi
+    from opfoundry_amd.abi import check, load_library
+    cfg = CONFIGS["indexer"]
+    x = make_indexer(cfg, dev)
+    B, s_q, H_I, seq = cfg["B"], cfg["s_q"], cfg["H_I"], cfg["seq"]
+    a = abi.IndexerArgs()
+    a.q, a.weights, a.k_cache = x["q"].data_ptr(), x["w"].data_ptr(), x["k"].data_ptr()
+    a.q_stride_b, a.q_stride_t, a.q_stride_h = x["q"].stride(0), x["q"].stride(1), x["q"].stride(2)
+    a.k_total_rows, a.k_stride_row = x["k"].shape[0], 128
+    a.block_table, a.block_table_stride, a.block_size = x["bt"].data_ptr(), x["bt"].stride(0), x["bs"]
+    a.seq_lens, a.scores, a.score_stride = x["sl"].data_ptr(), x["scores"].data_ptr(), seq
+    a.B, a.s_q, a.H_I, a.n_cols, a.causal = B, s_q, H_I, seq, 1
+    fn = load_library().dsa_indexer_scores
+    ap = ctypes.byref(a)
+    st = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        rc = fn(ap, st)
+        if rc:
+            check(rc, "dsa_indexer_scores")
+    ms = time_steps(step, args.steps, args.warmup)
+    pairs = sum(seq - (s_q - 1 - t) for t in range(s_q)) * B        # (token, position) pairs
+    alg = B * seq * 256 + pairs * 4 + x["q"].numel() * 2 + x["w"].numel() * 4
+    flops = 2 * 128 * H_I * pairs
+    ach = alg / (ms * 1e-3) / 1e9
+    leg = {"workload": f"indexer: {NAMES['indexer']}", "us_per_step": round(ms * 1e3, 3),
+           "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+           "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": profiled_traffic("dsa_indexer_traffic.txt"),
+                        "kernel": "dsa_indexer_kernel<64>", "kernel_avg_us": round(ms * 1e3, 3), "alg_bytes": alg,
+                        "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}}
+    if not args.no_cpu:
+        import oracle
+        try:
+            from threadpoolctl import threadpool_info
+            nt = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+        except Exception:
+            nt = 1
+        nb = 4
+        qn = x["q"][:nb].cpu().view(torch.int16).numpy().view(np.uint16)
+        wn = x["w"][:nb].cpu().numpy()
+        rows = (x["bt"][:nb].long()[:, :, None] * x["bs"] + torch.arange(x["bs"], device=dev)).view(nb, -1)
+        kn = x["k"][rows.view(-1)].cpu().view(torch.int16).numpy().view(np.uint16)
+        t0 = time.perf_counter()
+        oracle.indexer_scores(qn, wn, kn, x["sl"][:nb].cpu().numpy(), k_batch_stride=seq, causal=True, n_cols=seq)
+        dt = time.perf_counter() - t0
+        leg["cpu_baseline"] = dict(value=dt * B / nb * 1e6, unit="us/step", cores=nt, kind="port",
+                                   cpu_model=cpu_model(),
+                                   sample=f"{nb} of {B} sequences (both tokens, all positions; float64 numpy, "
+                                          f"{nt} BLAS threads), {dt:.2f} s, scaled x{B / nb:.0f}")
+    del x
+    torch.cuda.empty_cache()
+    return leg
+
+
 # -------------------------------------------------------------- CPU baseline
 
 def cpu_baseline_decode(d, fmt_fp8, sample_queries, unit_scale):
@@ -923,6 +1006,13 @@ def main():
         ms = time_steps(v4_step(v, dev)[0], args.steps, args.warmup)
         print(json.dumps({"config": args.config, "ms_per_step": ms}))
         return
+    if cfg["kind"] == "indexer":
+        if not args.kernel_only:
+            ap.error("--config indexer is reported inside the default JSON line; use it with --kernel-only")
+        args.no_cpu = True
+        leg = indexer_leg(args, dev)
+        print(json.dumps({"config": args.config, "ms_per_step": leg["us_per_step"] / 1e3}))
+        return
     if cfg["kind"] == "topk":
         if not args.kernel_only:
             ap.error("--config topk is reported inside the default JSON line; use it with --kernel-only")
@@ -1025,6 +1115,8 @@ def main():
                 res["decode_legs"][name] = decode_leg(name, args, dev)
         log("csr_skew leg (device work plan against uniform splits)")
         res["csr_skew"] = csr_skew_leg(args, dev)
+        log("indexer leg")
+        res["indexer"] = indexer_leg(args, dev)
 
     if not args.no_mx:
         log("building mx (MXFP8 split-stream) inputs")
