@@ -41,7 +41,6 @@ namespace {
 
 constexpr int D_QK = DSA_MLA_D_QK;
 constexpr int D_NOPE = DSA_MLA_D_NOPE;
-constexpr int D_ROPE = DSA_MLA_D_ROPE;
 constexpr int D_VO = DSA_MLA_D_VO;
 constexpr int HEADS = 128;                 // heads per workgroup (4 waves x 32)
 constexpr int NWAVE = 4;
@@ -76,7 +75,6 @@ constexpr int RAW_STRIDE = FP8_LOADS * 1024;         // raw slot padded to whole
 constexpr int FP8_LPW = (FP8_LOADS + NWAVE - 1) / NWAVE;  // loads of wave 0 (6); the others 5
 constexpr int BF16_LPW = TILE / NWAVE + 1;           // 8 NoPE rows + one 8-row RoPE block
 constexpr int FP8_SCALE_OFF = D_NOPE;                // 4 fp32 scales
-constexpr int32_t POOL2 = dsa_rows::POOL2;           // row-list tag: a row of the second pool (V4 extend)
 constexpr int FP8_ROPE_OFF = D_NOPE + 16;            // 64 bf16 RoPE values
 // MXFP8 raw slot, one region per stream (every DMA load reads one stream):
 // NoPE codes of row r at 512 r (loads 0..15, two rows each), RoPE at
