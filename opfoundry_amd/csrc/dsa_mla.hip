@@ -181,6 +181,7 @@ struct FwdParams {
     int32_t causal;              // 1: decode rule  j <= L - s_q + t
                                  // 2: prefill rule j <= b + causal_offset
     int64_t causal_offset;
+    int32_t reverse;             // 1: workgroup x takes query token B-1-x (prefill)
     float scale_log2;            // sm_scale * log2(e)
 };
 
@@ -292,7 +293,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // under a CSR plan, an entry of the plan's item table.
     const int gx = p.hgroups == 1 ? (int)blockIdx.x : (int)blockIdx.x / p.hgroups;
     const int hbase = p.hgroups == 1 ? 0 : HEADS * ((int)blockIdx.x % p.hgroups);
-    int b = gx, t = blockIdx.y;
+    // Prefill runs its tokens last to first: later tokens see more rows, and
+    // with the longest lists dispatched first the CUs finish together instead
+    // of idling behind the last long workgroups.
+    int b = p.reverse ? (int)(gridDim.x / p.hgroups) - 1 - gx : gx, t = blockIdx.y;
     const int split = blockIdx.z;
     int item_k0 = 0, item_k1 = 0, item_slot = -1;
     if (p.plan_items) {
@@ -2024,6 +2028,7 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* a, void* ws, size_t ws_bytes, vo
     fp.B = a->N; fp.s_q = 1; fp.topk = a->topk; fp.chunk = a->topk;
     fp.causal = a->causal ? 2 : 0;
     fp.causal_offset = a->causal_offset;
+    fp.reverse = 1;
     fp.scale_log2 = a->sm_scale * LOG2E;
     return launch_fwd(fp, a->kv_format, a->N, 1, 1, (hipStream_t)stream);
 }

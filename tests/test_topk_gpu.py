@@ -120,3 +120,17 @@ def test_topk_feeds_decode(dev):
     torch.cuda.synchronize()
     o = o.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
     assert_parity(o, lse.cpu().numpy(), o_ref, l_ref, "decode of GPU-selected top-k lists")
+
+
+@pytest.mark.parametrize("n,k", [(65536, 2048), (65537, 2048), (100003, 2048), (100003, 5000)])
+def test_topk_row_length_paths(dev, n, k):
+    """Rows of at most 65536 positions are selected from registers, longer rows by the
+    two-read kernel (with its multi-pass path above 4096): both sides of the switch,
+    and ties at the threshold, against the oracle."""
+    print(f"[case] topk row length n={n} k={k}", flush=True)
+    rng = np.random.default_rng(n + k)
+    T = 6
+    scores = rng.standard_normal((T, n)).astype(np.float32)
+    scores[1] = np.round(scores[1] * 4.0)       # heavy ties
+    lengths = np.array([n, n - 1, n // 2, k + 1, k, 3], np.int32)
+    run_case(dev, scores, lengths, k)
