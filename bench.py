@@ -1191,7 +1191,7 @@ def main():
                        "roofline": {"bound": "hbm", "achieved": round(tach, 1), "peak": HBM_PEAK_GBS,
                                     "unit": "GB/s", "frac": round(tach / HBM_PEAK_GBS, 4),
                                     "traffic": profiled_traffic("dsa_topk_traffic.txt"),
-                                    "kernel": "dsa_topk_kernel", "kernel_avg_us": round(tk_ms * 1e3, 3),
+                                    "kernel": "dsa_topk_reg_kernel", "kernel_avg_us": round(tk_ms * 1e3, 3),
                                     "alg_bytes": t_bytes}}
         if not args.no_cpu:
             log("CPU baseline (oracle) on a topk sample")
