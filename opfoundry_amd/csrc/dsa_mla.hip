@@ -80,7 +80,10 @@ constexpr int FP8_ROPE_OFF = D_NOPE + 16;            // 64 bf16 RoPE values
 // NoPE codes of row r at 512 r (loads 0..15, two rows each), RoPE at
 // MX_ROPE_OFF + 128 r (loads 16..19, eight rows each), the 16 E8M0 scales at
 // MX_SC_OFF + 16 r (load 20; its upper 32 lanes repeat rows 0..31 into the
-// slot's padding).  Same 21 loads per tile as the 656-B rows.
+// slot's padding).  Same 21 loads per tile as the 656-B rows.  In the V3.2
+// format the 16-byte pieces of a row are permuted: NoPE piece c of row r at
+// position c ^ (r & 15), RoPE piece c at c ^ (r & 7), so that the QK^T reads
+// of one piece over 16 rows hit distinct bank groups.
 constexpr int MX_ROPE_OFF = TILE * D_NOPE;            // 16384
 constexpr int MX_SC_OFF = MX_ROPE_OFF + TILE * 128;   // 20480
 static_assert(MX_SC_OFF + 1024 <= 21 * 1024, "MXFP8 raw slot fits the 656-B slot");
@@ -100,6 +103,9 @@ struct Lay {
     // scales follow them in the same 512-byte stream row, then 64 bf16 RoPE)
     static constexpr bool MX = FMT == DSA_KV_MXFP8 || FMT == DSA_KV_MXFP8_V4;
     static constexpr bool V4MX = FMT == DSA_KV_MXFP8_V4;
+    // MXFP8 split streams (V3.2): the NoPE part of QK^T runs as scaled fp8
+    // MFMAs straight from the raw slot (Q and K both carry E8M0 blocks of 32)
+    static constexpr bool SQK = FMT == DSA_KV_MXFP8;
     // fp8 caches (any): raw-tile ring, dequant stage into the tile buffers
     static constexpr bool FP8 = F16 || MX;
     // 512-value rows: K = V = the whole row (V4 prefill)
@@ -196,6 +202,22 @@ struct DeqPiece {
     u32x4 v;
 };
 constexpr int DEQ_PIECES = TILE / NWAVE + 1;
+
+// fp8 e4m3 x e4m3, 32x32x64, with E8M0 block scales: byte `sel` of sa / sb
+// (a constant once the caller's loop is unrolled)
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+template <int SEL>
+__device__ __forceinline__ f32x16 mfma_scale8_sel(i32x8 a, i32x8 b, f32x16 c, int sa, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, SEL, sa, SEL, sb);
+}
+__device__ __forceinline__ f32x16 mfma_scale8(int sel, i32x8 a, i32x8 b, f32x16 c, int sa, int sb) {
+    switch (sel) {
+        case 0: return mfma_scale8_sel<0>(a, b, c, sa, sb);
+        case 1: return mfma_scale8_sel<1>(a, b, c, sa, sb);
+        case 2: return mfma_scale8_sel<2>(a, b, c, sa, sb);
+        default: return mfma_scale8_sel<3>(a, b, c, sa, sb);
+    }
+}
 
 __device__ __forceinline__ f32x16 mfma_bf16(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
@@ -325,7 +347,24 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // Issued first so their latency overlaps the index resolution below.
     u32x4 qf[L::KS];
     u32x4 q_scales = {0, 0, 0, 0};   // MXFP8: the 16 E8M0 scales of this head's Q
-    if constexpr (L::MX) {
+    unsigned q_sc8[2] = {0u, 0u};    // scaled QK^T: the E8M0 bytes of blocks 2 k8 + hi (k8 = 4 i + byte)
+    if constexpr (L::SQK) {
+        // B operand of the scaled fp8 MFMA (64-deep k-steps k8): lane (head,
+        // hi) holds codes 64 k8 + 16 hi .. +15 and 64 k8 + 32 + 16 hi .. +15,
+        // in qf[2 k8] and qf[2 k8 + 1]; RoPE as bf16 in qf[KS_NOPE ..]
+        const unsigned char* q8p = p.q8 + (int64_t)b * p.q8_sb + (int64_t)t * p.q8_st + (int64_t)head_q * p.q8_sh + 16 * hi;
+#pragma unroll
+        for (int k8 = 0; k8 < KS_NOPE / 4; ++k8) {
+            qf[2 * k8] = *reinterpret_cast<const u32x4*>(q8p + 64 * k8);
+            qf[2 * k8 + 1] = *reinterpret_cast<const u32x4*>(q8p + 64 * k8 + 32);
+        }
+        q_scales = *reinterpret_cast<const u32x4*>(p.qsc + (int64_t)b * p.qsc_sb + (int64_t)t * p.qsc_st +
+                                                   (int64_t)head_q * p.qsc_sh);
+        const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head_q * p.q_sh + 8 * hi;
+#pragma unroll
+        for (int ks = KS_NOPE; ks < L::KS; ++ks)
+            qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * (ks - KS_NOPE));
+    } else if constexpr (L::MX) {
         // fp8 codes of dims 16ks + 8hi .. +7 in the low half of qf[ks],
         // converted to bf16 once they have landed; RoPE as bf16
         const unsigned char* q8p = p.q8 + (int64_t)b * p.q8_sb + (int64_t)t * p.q8_st + (int64_t)head_q * p.q8_sh + 8 * hi;
@@ -566,10 +605,14 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                                : (e2 ? q1 : q0) + r64 * p.kvr_st + 16 * (ln & 7);
                     lds_dma16(src, RING + slot * RAW_STRIDE + 1024 * k);
                 } else if constexpr (L::MX) {
-                    // one stream per load: base and row stride are wave-uniform
+                    // one stream per load: base and row stride are wave-uniform;
+                    // lane ln's piece is the one its slot position holds (the
+                    // permutation above)
+                    const int rn = 2 * k + (ln >> 5), rr = 8 * (k - 16) + (ln >> 3);
                     const unsigned char* src =
-                        k < 16 ? p.kv + row * p.kvn_st + 16 * (ln & 31)
-                               : (k < 20 ? p.kv_ro + row * p.kvr_st + 16 * (ln & 7) : p.kv_sc + row * p.kvs_st);
+                        k < 16 ? p.kv + row * p.kvn_st + 16 * ((ln & 31) ^ (rn & 15))
+                               : (k < 20 ? p.kv_ro + row * p.kvr_st + 16 * ((ln & 7) ^ (rr & 7))
+                                         : p.kv_sc + row * p.kvs_st);
                     lds_dma16(src, RING + slot * RAW_STRIDE + 1024 * k);
                 } else {
                     lds_dma16(p.kv + (row * (uint64_t)p.row_bytes + ((unsigned)opaque((int)f_rc[i]) >> 16)),
@@ -617,7 +660,8 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                 d.v = u32x4{lo[0], lo[1], hi8[0], hi8[1]};
                 return d;
             }
-            const u32x2 codes = lds_ld<u32x2>(rr + 8 * ln);
+            // (MXFP8: codes 8 ln.. are in piece ln / 2, at its permuted position)
+            const u32x2 codes = lds_ld<u32x2>(L::MX ? rr + 16 * ((ln >> 1) ^ (r & 15)) + 8 * (ln & 1) : rr + 8 * ln);
             d.v[0] = codes[0];
             d.v[1] = codes[1];
             if constexpr (L::MX) {
@@ -668,7 +712,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     };
     auto dequant = [&](lds_cptr rb, lds_ptr tb) {
 #pragma unroll
-        for (int j = 0; j < (L::D512 ? DEQ_PIECES - 1 : DEQ_PIECES); ++j) deq_store(tb, j, deq_load(rb, j));
+        for (int j = 0; j < (L::D512 || L::SQK ? DEQ_PIECES - 1 : DEQ_PIECES); ++j) deq_store(tb, j, deq_load(rb, j));
     };
 
     // ---- online softmax state (fixed reference max) ----
@@ -695,6 +739,11 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             for (int ks = 0; ks < KS_NOPE; ++ks)
 #pragma unroll
                 for (int w = 0; w < 4; ++w) qf[ks][w] = bf16x2_to_f16x2(qf[ks][w]);
+        } else if constexpr (L::SQK) {
+            // the codes stay fp8; the scale operands take, per lane, the bytes
+            // of blocks 2 k8 + hi: the even (hi = 0) or odd bytes of the 16
+            q_sc8[0] = __builtin_amdgcn_perm(q_scales[1], q_scales[0], hi ? 0x07050301u : 0x06040200u);
+            q_sc8[1] = __builtin_amdgcn_perm(q_scales[3], q_scales[2], hi ? 0x07050301u : 0x06040200u);
         } else if constexpr (L::MX) {
             // fp8 NoPE of Q -> bf16: dims 16ks + 8hi .. +7 lie in scale block ks / 2
 #pragma unroll
@@ -786,6 +835,50 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         return acc;
     };
 
+    // ---- MXFP8 (V3.2) S^T = K Q^T straight from the raw slot of the tile ----
+    // NoPE: 8 scaled fp8 MFMAs (v_mfma_scale_f32_32x32x64_f8f6f4, 64-deep):
+    // lane (hi, lr) holds row lr's codes 64 k8 + 16 hi .. +15 and
+    // 64 k8 + 32 + 16 hi .. +15, and its scale byte k8 % 4 of k_sc8[k8 / 4] is
+    // row lr's E8M0 of block 2 k8 + hi (Q the same way); the MFMA applies
+    // both scales per 32-block.  RoPE: 4 bf16 MFMAs from the raw RoPE stream.
+    auto qk8 = [&](lds_cptr raw, auto&& per_step) -> f32x16 {
+        const int ln = lane;
+        const int lhi = ln >> 5, lr = ln & 31;
+        const lds_cptr kn = raw + lr * D_NOPE;
+        const int sw = lr & 15;
+        const u32x4 ksc = lds_ld<u32x4>(raw + MX_SC_OFF + 16 * lr);
+        auto k_frag = [&](int k8) -> i32x8 {
+            const u32x4 a0 = lds_ld<u32x4>(kn + 16 * ((4 * k8 + lhi) ^ sw));
+            const u32x4 a1 = lds_ld<u32x4>(kn + 16 * ((4 * k8 + 2 + lhi) ^ sw));
+            return __builtin_bit_cast(i32x8, __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7));
+        };
+        auto q_frag = [&](int k8) -> i32x8 {
+            return __builtin_bit_cast(i32x8, __builtin_shufflevector(qf[2 * k8], qf[2 * k8 + 1], 0, 1, 2, 3, 4, 5, 6, 7));
+        };
+        i32x8 kb[2] = {k_frag(0), k_frag(1)};
+        const unsigned sel = lhi ? 0x07050301u : 0x06040200u;
+        const int k_sc8[2] = {(int)__builtin_amdgcn_perm(ksc[1], ksc[0], sel), (int)__builtin_amdgcn_perm(ksc[3], ksc[2], sel)};
+        f32x16 acc = {};
+#pragma unroll
+        for (int k8 = 0; k8 < KS_NOPE / 4; ++k8) {
+            __builtin_amdgcn_sched_barrier(0);
+            acc = mfma_scale8(k8 & 3, kb[k8 & 1], q_frag(k8), acc, k_sc8[k8 >> 2], (int)q_sc8[k8 >> 2]);
+            if (k8 + 2 < KS_NOPE / 4) kb[k8 & 1] = k_frag(k8 + 2);
+            per_step(k8);
+        }
+        const lds_cptr kr = raw + MX_ROPE_OFF + 128 * lr;
+        const int rsw = lr & 7;
+        u32x4 rb[2] = {lds_ld<u32x4>(kr + 16 * (lhi ^ rsw)), lds_ld<u32x4>(kr + 16 * ((2 + lhi) ^ rsw))};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            __builtin_amdgcn_sched_barrier(0);
+            acc = mfma_bf16(rb[j & 1], qf[KS_NOPE + j], acc);
+            if (j + 2 < 4) rb[j & 1] = lds_ld<u32x4>(kr + 16 * ((2 * (j + 2) + lhi) ^ rsw));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        return acc;
+    };
+
     // ---- fp8 caches, one tile: QK^T (after the gathers of a later tile), softmax, PV (+ dequant of the next tile) ----
     // kt: buffer holding tile `it`; nxt: buffer receiving tile it+1.
     bool first_tile = true;
@@ -799,7 +892,9 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         // Gathers of tile it+NPRE, all at once: the tile barrier just before
         // has drained this wave's LDS accesses, and an LDS-DMA load issued
         // while LDS reads are in flight holds the wave far longer.
-        if (do_issue) issue_rows(gcur, issue_slot);
+        // (MXFP8 V3.2: after the P barrier, into this tile's own raw slot)
+        if constexpr (!L::SQK)
+            if (do_issue) issue_rows(gcur, issue_slot);
         __builtin_amdgcn_sched_barrier(0);
         // V4 fp8 rows: the next tile's dequant runs between the QK^T MFMAs
         // (piece j loads at k-step 4j, is converted and stored at 4j + 2):
@@ -809,12 +904,19 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         DeqPiece dq[2];
         const lds_cptr draw = FP8 ? RING + ((it + 1) % 3) * RAW_STRIDE : kt;
         constexpr int NPIECE = L::D512 ? DEQ_PIECES - 1 : DEQ_PIECES;
-        f32x16 sacc = qk(kt, [&](int ks) {
-            if constexpr (DEQ_QK) {
-                if ((ks & 3) == 0 && ks / 4 < NPIECE) dq[(ks / 4) & 1] = deq_load(draw, ks / 4);
-                if ((ks & 3) == 2 && ks / 4 < NPIECE) deq_store(nxt, ks / 4, dq[(ks / 4) & 1]);
+        // MXFP8 V3.2: K straight from this tile's raw slot (scaled fp8 MFMAs)
+        f32x16 sacc = [&]() -> f32x16 {
+            if constexpr (L::SQK) {
+                return qk8(RING + (it % 3) * RAW_STRIDE, [](int) {});
+            } else {
+                return qk(kt, [&](int ks) {
+                    if constexpr (DEQ_QK) {
+                        if ((ks & 3) == 0 && ks / 4 < NPIECE) dq[(ks / 4) & 1] = deq_load(draw, ks / 4);
+                        if ((ks & 3) == 2 && ks / 4 < NPIECE) deq_store(nxt, ks / 4, dq[(ks / 4) & 1]);
+                    }
+                });
             }
-        });
+        }();
         // row ids of the tile issued in the next step
         if (it + NPRE + 1 < ntiles) gnext = load_rows(it + NPRE + 1);
 
@@ -864,6 +966,12 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         p_store(0);
         p_store(1);
         tile_barrier();     // every wave's P is visible
+        if constexpr (L::SQK) {
+            // every wave is done with this tile's raw slot: refill it
+            __builtin_amdgcn_sched_barrier(0);
+            if (do_issue) issue_rows(gcur, issue_slot);
+            __builtin_amdgcn_sched_barrier(0);
+        }
 
         // ---- O^T[128 dims of this wave x 128 heads] += V^T P^T ----
         // Transposed V reads: 16-lane group g16 reads rows R..R+3 (lane
@@ -908,7 +1016,8 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                 static_assert(DEQ_PIECES == 9, "dequant pieces vs MFMA groups");
                 __builtin_amdgcn_sched_barrier(0);
                 deq_store(nxt, 7, dq[1]);
-                if constexpr (!L::D512) deq_store(nxt, 8, deq_load(draw, 8));   // RoPE block
+                // RoPE block (MXFP8 V3.2: QK^T reads it from the raw slot)
+                if constexpr (!L::D512 && !L::SQK) deq_store(nxt, 8, deq_load(draw, 8));
             }
         }
         __builtin_amdgcn_sched_barrier(0);

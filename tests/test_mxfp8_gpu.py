@@ -12,9 +12,11 @@ in tests/test_oracle_mxfp8.py) with the bar of every parity test:
 - LSE within 1e-3 * (1 + |LSE|).
 
 Two more checks:
-- MXFP8 values dequantise exactly to bf16 and the kernel runs the bf16
-  kernel's arithmetic on them, so its outputs equal the bf16 CSR entry's on
-  the dequantised rows bit for bit;
+- MXFP8 values dequantise exactly to bf16, so the bf16 CSR entry on the
+  dequantised rows is a second reference: the NoPE part of QK^T runs as
+  scaled fp8 MFMAs (block dot products accumulated inside the MFMA, not
+  bit-identical to fp32 sums), and the outputs agree with the bf16 entry's to
+  the same bar;
 - padded streams (non-dense strides) give the same results.
 """
 from __future__ import annotations
@@ -114,10 +116,10 @@ def test_mxfp8_reference_harness_shape(dev):
     print(f"[case] {len(pick)} sampled batches: max|dO|={e[0]:.3e} max rel dLSE={e[1]:.3e}", flush=True)
 
 
-def test_mxfp8_equals_bf16_entry_bitwise(dev):
-    """The dequantised rows and queries are bf16 values; the bf16 CSR entry on them must give
-    the MXFP8 entry's outputs bit for bit."""
-    print("[case] mxfp8 vs bf16 CSR entry, bitwise", flush=True)
+def test_mxfp8_matches_bf16_entry(dev):
+    """The dequantised rows and queries are bf16 values; the bf16 CSR entry on them agrees with
+    the MXFP8 entry's outputs to the parity bar (with 1 and 2 splits)."""
+    print("[case] mxfp8 vs bf16 CSR entry", flush=True)
     lens = [1500, 900, 33]
     q, kv, indptr, indices = mx_case(53, lens, 1, 4096)
     qd, kvd = dev_streams(q, kv, dev)
@@ -129,8 +131,8 @@ def test_mxfp8_equals_bf16_entry_bitwise(dev):
                                       torch.from_numpy(indptr).to(dev), torch.from_numpy(indices).to(dev),
                                       SM_SCALE, s_q=1, num_splits=ns)
         torch.cuda.synchronize()
-        assert (bits(out) == o_mx).all(), f"splits={ns}"
-        assert np.array_equal(lse.cpu().numpy(), l_mx), f"splits={ns}"
+        e = assert_parity(o_mx, l_mx, bits(out), lse.cpu().numpy(), f"mxfp8 vs bf16 entry splits={ns}")
+        print(f"[case] splits={ns}: max|dO|={e[0]:.3e} max rel dLSE={e[1]:.3e}", flush=True)
 
 
 def test_mxfp8_padded_streams(dev):
