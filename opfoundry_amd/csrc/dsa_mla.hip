@@ -322,10 +322,20 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     const int split = blockIdx.z;
     int item_k0 = 0, item_k1 = 0, item_slot = -1;
     if (p.plan_items) {
+        // Items are in row order, so the s_q rows of a batch (MTP tokens with
+        // one list) are consecutive items.  Workgroups go to the 8 XCDs in
+        // turn: within each group of 8 s_q workgroups, item s_q c + u runs on
+        // XCD c, so a batch's tokens share that XCD's L2 and its rows are
+        // fetched from HBM once.  (The grid is a multiple of 8 s_q.)
+        int item = gx;
+        if (p.hgroups == 1) {
+            const int G = 8 * p.s_q, j = gx / G, rem = gx - j * G;
+            item = G * j + p.s_q * (rem & 7) + (rem >> 3);
+        }
         // the grid covers the most items a plan can hold: past the plan's
         // count the whole workgroup leaves before any barrier
-        if (gx >= __builtin_amdgcn_readfirstlane(p.plan_hdr[0])) return;
-        const int4 w = p.plan_items[gx];
+        if (item >= __builtin_amdgcn_readfirstlane(p.plan_hdr[0])) return;
+        const int4 w = p.plan_items[item];
         const int qrow_i = __builtin_amdgcn_readfirstlane(w.x);
         b = qrow_i / p.s_q;
         t = qrow_i - b * p.s_q;
@@ -1784,7 +1794,9 @@ int csr_plan_launch(FwdParams& fp, int fmt, int max_len, void* ws, bool build, h
         fp.part_o = (float*)(w + L.po);
         fp.part_lse = (float*)(w + L.pl);
     }
-    const int r = launch_fwd(fp, fmt, L.items_max, 1, 1, st);
+    // (a multiple of 8 s_q workgroups: the item order the kernel maps them to)
+    const int G = 8 * fp.s_q;
+    const int r = launch_fwd(fp, fmt, (L.items_max + G - 1) / G * G, 1, 1, st);
     if (r || !L.slots_max) return r;
     hipLaunchKernelGGL(dsa_mla_combine_plan_kernel, dim3(4 * PLAN_TARGET), dim3(256), 0, st, (const float*)fp.part_o,
                        (const float*)fp.part_lse, fp.H, fp.s_q, fp.out, fp.o_sb, fp.o_st, fp.o_sh, fp.lse,
