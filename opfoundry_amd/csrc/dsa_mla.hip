@@ -724,6 +724,52 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 #pragma unroll
         for (int j = 0; j < (L::D512 || L::SQK ? DEQ_PIECES - 1 : DEQ_PIECES); ++j) deq_store(tb, j, deq_load(rb, j));
     };
+    // The same NoPE dequant split by output dims (656-B rows, MXFP8 V3.2):
+    // piece g = 4u + m of wave w is rows 16u .. 16u + 15, dims
+    // 128w + 32m .. +31 - exactly the V block that PV group (u, m) of wave w
+    // reads; lane l converts row 16u + l/4, dims d0 = 128w + 32m + 8(l % 4)
+    // .. +7.  A wave writes only dims it reads itself in PV, so a tile buffer
+    // is refilled by its own PV readers, each piece once that wave has read it.
+    auto deqd_load = [&](lds_cptr rb, int g) -> DeqPiece {
+        const int ln = opaque(lane);
+        const int r = 16 * (g >> 2) + (ln >> 2);
+        const int d0 = 128 * wave + 32 * (g & 3) + 8 * (ln & 3);
+        DeqPiece d;
+        u32x2 codes;
+        if constexpr (L::MX) {
+            // piece d0 / 16 of the row, at its permuted position
+            codes = lds_ld<u32x2>(rb + D_NOPE * r + 16 * ((d0 >> 4) ^ (r & 15)) + 8 * ((d0 >> 3) & 1));
+            d.v[2] = lds_ld<unsigned char>(rb + MX_SC_OFF + 16 * r + (d0 >> 5));
+        } else {
+            const lds_cptr rr = rb + r * FP8_ROW;
+            codes = lds_ld<u32x2>(rr + d0);
+            d.v[2] = __float_as_uint(lds_ld<float>(rr + FP8_SCALE_OFF + 4 * wave));
+        }
+        d.v[0] = codes[0];
+        d.v[1] = codes[1];
+        d.v[3] = 0;
+        return d;
+    };
+    auto deqd_store = [&](lds_ptr tb, int g, const DeqPiece& d) {
+        const int ln = opaque(lane);
+        const int r = 16 * (g >> 2) + (ln >> 2);
+        const int ch = 16 * wave + 4 * (g & 3) + (ln & 3);    // 16-byte chunk: dims 8 ch .. 8 ch + 7
+        u32x4 out;
+        if constexpr (L::MX) {
+            out = mx_to_bf16(d.v[0], d.v[1], d.v[2]);
+        } else {
+            const float sc = __uint_as_float(d.v[2]);
+            const _Float16 m16 = (_Float16)__uint_as_float((d.v[2] & 0x007FFFFFu) | 0x3F800000u);
+            const f16x2 mm = {m16, m16};
+            const f16x2 h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)d.v[0], sc, false) * mm;
+            const f16x2 h1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)d.v[0], sc, true) * mm;
+            const f16x2 h2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)d.v[1], sc, false) * mm;
+            const f16x2 h3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)d.v[1], sc, true) * mm;
+            out = u32x4{__builtin_bit_cast(unsigned, h0), __builtin_bit_cast(unsigned, h1),
+                        __builtin_bit_cast(unsigned, h2), __builtin_bit_cast(unsigned, h3)};
+        }
+        lds_st<u32x4>(tb + r * NOPE_STRIDE + 16 * (ch ^ nope_sw(r)), out);
+    };
 
     // ---- online softmax state (fixed reference max) ----
     // p = exp2(s*c - m_ref) with m_ref fixed for the whole pass (the first
@@ -1087,7 +1133,11 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // O^T += V^T P^T for the tile in kv_t with P from px_cur; with_exp
     // (std::true_type): the numerators of the next tile's scores sn go to en,
     // two per MFMA group (group (u, m) gives en[8u + 2m], en[8u + 2m + 1])
-    auto pv_pipe = [&](lds_cptr kv_t, lds_cptr px_cur, const f32x16& sn, float* en, auto with_exp) {
+    // with_deq (std::true_type): piece g = 4u + m of the tile in raw slot draw
+    // is dequantised into tbd (kv_t itself) in group (u, m), stored after the
+    // group's MFMAs have consumed this wave's V block (u, m)
+    auto pv_pipe = [&](lds_cptr kv_t, lds_cptr px_cur, const f32x16& sn, float* en, auto with_exp,
+                       lds_cptr draw, lds_ptr tbd, auto with_deq) {
         const int ln = lane;
         const int lhi = ln >> 5;
         const int g16 = ln >> 4, i16 = ln & 15, rr = i16 >> 2, pp = i16 & 3;
@@ -1109,6 +1159,8 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             for (int m = 0; m < 4; ++m) {
                 __builtin_amdgcn_sched_barrier(0);
                 const u32x4 va_nxt = m + 1 < 4 ? v_frag(u, m + 1) : va_cur;
+                DeqPiece dq;
+                if constexpr (decltype(with_deq)::value) dq = deqd_load(draw, 4 * u + m);
 #pragma unroll
                 for (int h = 0; h < NWAVE; ++h) mfma_o<L::F16>(o[4 * m + h], va_cur, pbf[h]);
                 if constexpr (decltype(with_exp)::value) {
@@ -1116,6 +1168,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                     en[r0] = __builtin_amdgcn_exp2f(__builtin_fmaf(sn[r0], c_s, -m_ref));
                     en[r0 + 1] = __builtin_amdgcn_exp2f(__builtin_fmaf(sn[r0 + 1], c_s, -m_ref));
                 }
+                if constexpr (decltype(with_deq)::value) deqd_store(tbd, 4 * u + m, dq);
                 va_cur = va_nxt;
             }
         }
@@ -1141,7 +1194,92 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             for (int s = 0; s < NPRE; ++s)
                 if (s < ntiles) issue_rows(load_rows(s), s);
             if (NPRE < ntiles) gnext = load_rows(NPRE);
-            if constexpr (FP8) {
+            if constexpr (L::SQK) {
+                // Pipelined (MXFP8 V3.2).  Iteration j: QK^T of
+                // tile j; PV of tile j-1 with tile j's softmax numerators and
+                // tile j+1's dequant between its MFMAs (by output dims, into the
+                // buffer PV reads: buffer j % 2 holds tile j); a barrier; the
+                // gathers of tile j+3 into tile j's raw slot; tile j's P.  K of
+                // tile j: buffer j % 2, or (MXFP8) raw slot j % 3.
+                auto deq_tile = [&](lds_cptr rb, lds_ptr tb) {
+#pragma unroll
+                    for (int g = 0; g < 8; ++g) deqd_store(tb, g, deqd_load(rb, g));
+                    if constexpr (!L::SQK) deq_store(tb, 8, deq_load(rb, 8));   // RoPE block
+                };
+                if (ntiles > 0) {
+                    wait_tiles(min(ntiles, NPRE) - 1);    // tile 0 landed (1, 2 may be in flight)
+                    tile_barrier();
+                    deq_tile(RING, T0);
+                    // iteration 0: no PV yet; tile 1 is dequantised on its own
+                    wait_tiles(2 < ntiles ? 1 : 0);       // tile 1 landed
+                    tile_barrier();
+                    f32x16 s0 = [&]() -> f32x16 {
+                        if constexpr (L::SQK) return qk8(RING, [](int) {});
+                        else return qk(T0, [](int) {});
+                    }();
+                    if (first_tile) {
+                        m_ref = first_max(s0, n_valid) * c_s;
+                        first_tile = false;
+                    }
+                    mask_track(s0, 0);
+                    if (nchunks == 1 && ntiles == 1) {
+                        // one-tile list: the exact sum folded into the reference
+                        float lt = 0.0f;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) lt += __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], c_s, -m_ref));
+                        lt += __shfl_xor(lt, 32, 64);
+                        m_ref = m_ref + __builtin_amdgcn_logf(lt);
+                    }
+                    float e0[16];
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) e0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], c_s, -m_ref));
+                    if (ntiles > 1) deq_tile(RING + RAW_STRIDE, T1);
+                    tile_barrier();    // every wave is done with tile 0's raw slot
+                    if (NPRE < ntiles) {
+                        issue_rows(gnext, 0);
+                        if (NPRE + 1 < ntiles) gnext = load_rows(NPRE + 1);
+                    }
+                    p_half(e0, 0, PX);
+                    p_half(e0, 1, PX);
+                }
+                for (int j = 1; j < ntiles; ++j) {
+                    // tile j+1 landed (dequantised below); tile j+2 may be in flight.
+                    // The barrier publishes tile j's dequant and tile j-1's P.
+                    wait_tiles(j + 2 < ntiles ? 1 : 0);
+                    tile_barrier();
+                    const lds_ptr tq = (j & 1) ? T1 : T0;     // tile j
+                    const lds_ptr tv = (j & 1) ? T0 : T1;     // tile j-1, refilled with tile j+1
+                    f32x16 sn = [&]() -> f32x16 {
+                        if constexpr (L::SQK) return qk8(RING + (j % 3) * RAW_STRIDE, [](int) {});
+                        else return qk(tq, [](int) {});
+                    }();
+                    mask_track(sn, j);
+                    float en[16];
+                    // (after the last tile the dequant converts whatever the slot
+                    // holds into a buffer that is not read again: no branch
+                    // splits the MFMA groups)
+                    const lds_cptr dr = RING + ((j + 1) % 3) * RAW_STRIDE;
+                    pv_pipe(tv, PX, sn, en, std::true_type{}, dr, tv, std::true_type{});
+                    if constexpr (!L::SQK) deq_store(tv, 8, deq_load(dr, 8));   // RoPE block of tile j+1
+                    // every wave is done with tile j-1's P and V and tile j's raw slot
+                    tile_barrier();
+                    if (j + NPRE < ntiles) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        issue_rows(gnext, (j + NPRE) % 3);
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (j + NPRE + 1 < ntiles) gnext = load_rows(j + NPRE + 1);
+                    }
+                    p_half(en, 0, PX);
+                    p_half(en, 1, PX);
+                }
+                if (ntiles > 0) {
+                    // the last tile: PV only (its P is published by this barrier)
+                    tile_barrier();
+                    float en[16];
+                    pv_pipe(((ntiles - 1) & 1) ? T1 : T0, PX, f32x16{}, en, std::false_type{}, RING, T0,
+                            std::false_type{});
+                }
+            } else if constexpr (FP8) {
                 if (ntiles > 0) {
                     // tile 0 landed (tiles 1, 2 may still be in flight)
                     wait_tiles(min(ntiles, NPRE) - 1);
@@ -1186,7 +1324,8 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                     if (it + NPRE + 1 < ntiles) gnext = load_rows(it + NPRE + 1);
                     mask_track(sn, it + 1);
                     float en[16];
-                    pv_pipe(slot_buf(slot_cur), PX + (it & 1) * PXB, sn, en, std::true_type{});
+                    pv_pipe(slot_buf(slot_cur), PX + (it & 1) * PXB, sn, en, std::true_type{}, RING, T0,
+                            std::false_type{});
                     const lds_ptr px_nxt = PX + ((it + 1) & 1) * PXB;
                     p_half(en, 0, px_nxt);
                     p_half(en, 1, px_nxt);
@@ -1196,7 +1335,8 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                     // the last tile: PV only (its P is published by this barrier)
                     tile_barrier();
                     float en[16];
-                    pv_pipe(slot_buf(slot_cur), PX + ((ntiles - 1) & 1) * PXB, f32x16{}, en, std::false_type{});
+                    pv_pipe(slot_buf(slot_cur), PX + ((ntiles - 1) & 1) * PXB, f32x16{}, en, std::false_type{}, RING,
+                            T0, std::false_type{});
                 }
             }
             // drain in-flight gathers before the ring can be reused or left
