@@ -12,18 +12,24 @@ float64 on C3-shaped data (656-B fp8 rows quantised from N(0,1), bf16 Q ~ N(0,1)
 and compares each with the oracle under the parity bar every GPU test uses
 (O: 2e-2 or one bf16 step where |O| >= 4; LSE: 1e-3 * (1 + |LSE|)).
 
-The exact-Q emulation passes with margin; both fp8-Q variants miss the O bar by
-2.5-4.5x and the LSE bar by 3-5x.  An fp8 NoPE QK would therefore fail the parity
+The exact-Q emulation passes; both fp8-Q variants miss the O bar by 2.5-4.5x and
+the LSE bar by 3-5x on 4 tokens.  On C3's full batch (256 tokens, 32,768 (token,
+head) rows; DSA_FP8QK_TOKENS=256) the worst errors are, as fractions of the bars
+(O, LSE): exact Q 0.78 / 0.0004, per-128 e4m3 Q 4.7 / 4.5, MX e4m3 Q 7.0 / 7.4.  An fp8 NoPE QK would therefore fail the parity
 the north-star workload is held to, whatever its speed.
 """
 from __future__ import annotations
+
+import os
 
 import numpy as np
 
 import oracle
 from _cases import fp8_rows, lse_rel, o_bound
 
-T, H, K = 4, 128, 2048
+# query tokens: 4 in the CPU suite; DSA_FP8QK_TOKENS=256 runs C3's full batch (128 x 2 MTP
+# tokens, all 32,768 (token, head) LSEs), about a minute of float64 numpy
+T, H, K = int(os.environ.get("DSA_FP8QK_TOKENS", "4")), 128, 2048
 SM = 1.0 / np.sqrt(192.0)
 
 
@@ -68,8 +74,9 @@ def test_fp8_q_misses_the_parity_bar():
     for mode in ("exact", "per128", "mx32"):
         o, lse = forward(qf, rows, mode)
         res[mode] = (float((np.abs(oracle.bf16_to_f32(o) - ref) / bound).max()), lse_rel(lse, l_ref) / 1e-3)
+    print(f"[case] T={T}: (worst O error / bound, worst LSE error / bar) {res}", flush=True)
     # (worst O error / bound, LSE error / bar): the shipped arithmetic passes ...
-    assert res["exact"][0] < 0.6 and res["exact"][1] < 0.01, res
+    assert res["exact"][0] < 1.0 and res["exact"][1] < 0.01, res
     # ... an e4m3 Q fails both bars, by a wide margin
     for mode in ("per128", "mx32"):
         assert res[mode][0] > 2.0 and res[mode][1] > 2.0, (mode, res)
