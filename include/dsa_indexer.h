@@ -56,7 +56,7 @@ typedef struct {
     const int32_t* seq_lens;     /* int32 [B] */
     float* scores;               /* fp32, row (b * s_q + t) at scores + row * score_stride */
     int64_t score_stride;
-    int32_t B, s_q, H_I;         /* H_I: a multiple of 32, at most 128 */
+    int32_t B, s_q, H_I;         /* H_I: 32, 64 or 128 (other counts: DSA_ERR_UNSUPPORTED) */
     int32_t n_cols;              /* positions scored per row: j < min(len, n_cols) */
     int32_t causal;
 } dsa_indexer_args;

@@ -13,6 +13,15 @@
  *                              [128g, 128g+128) and equals amax_g / 448
  *                    [528,656) 64 x bf16 RoPE                    =  656 B
  *   Dequantised value of NoPE dim d = float(e4m3(code_d)) * scale[d / 128].
+ *   Range: the kernels compute these rows in fp16 (K and V values, and Q's
+ *   NoPE part).  Any finite q is accepted: a head with |q| >= 2^15 is scaled
+ *   by a power of two into fp16's range and its softmax scale by the inverse,
+ *   which is exact.  Every scale of an attended row must lie in [0, 128)
+ *   (group amax below 57344, so every value stays below fp16's 65504); a
+ *   query token that attends a row with a scale of 128 or more, or a negative
+ *   or non-finite one, gets NaN O and LSE (a defined signal, never a silently
+ *   wrong attention).  Rows the cache writer produces from bf16 inputs with
+ *   group amax below 57344 always qualify.
  *
  * Index semantics (top-k form).  indices[b][t][k] is a logical position j in
  * sequence b.  It is valid iff 0 <= j < seq_lens[b] and, when causal != 0,
@@ -33,9 +42,11 @@
  * heads 0..H-1 only.
  *
  * Numerics.  Scores s = (q . k) * sm_scale in fp32; softmax probabilities are
- * rounded to bf16 before the P.V product, accumulation is fp32, O is written
- * as bf16 (round to nearest even) and LSE = max + ln(sum exp(s - max)) as
- * fp32 (natural log of the scaled scores).
+ * rounded to the P.V product's 16-bit type before it (bf16 for bf16 and MXFP8
+ * rows, as the reference does at host.cc:451; fp16 for DSA_KV_FP8_656 rows,
+ * whose V is fp16), accumulation is fp32, O is written as bf16 (round to
+ * nearest even) and LSE = max + ln(sum exp(s - max)) as fp32 (natural log of
+ * the scaled scores).
  *
  * Conventions.  All pointers are device pointers owned by the caller (the
  * workspace included); strides are in elements; `stream` is a hipStream_t
@@ -225,9 +236,14 @@ int dsa_mla_combine(const float* partial_o, const float* partial_lse, int32_t nu
  *            merges.  The workspace then holds the plan and at most 512
  *            partial rows (H x 513 fp32 each), none when max_kv_len <= 128.
  *            DSA_MLA_SPLITS_PLANNED (-1): as 0, with the plan already in the
- *            workspace (dsa_mla_csr_plan, or an earlier call with 0, on the
- *            same kv_indptr, B, s_q, H and max_kv_len): the plan is built once
- *            and reused by every layer of a decode step.
+ *            workspace (dsa_mla_csr_plan, or an earlier call with 0), built
+ *            from the same list lengths (kv_indptr) with the same B, s_q and
+ *            max_kv_len: the plan is built once and reused by every layer of a
+ *            decode step.  The kernels check the plan against the call: a
+ *            plan built for another B, s_q or max_kv_len makes every query
+ *            row's O and LSE NaN (nothing else is read or written), and a row
+ *            whose list length differs from the planned one gets NaN O and
+ *            LSE; a plan is never silently trusted.
  *            1..DSA_MLA_MAX_SPLITS: every row cut into num_splits equal
  *            parts (workspace: num_splits partial rows per row; none for 1).
  */

@@ -191,6 +191,15 @@ struct FwdParams {
     float scale_log2;            // sm_scale * log2(e)
 };
 
+// CSR work-plan item field w: bits 0..29 hold the partial slot + 1 (0: the
+// item writes its row's output directly), bit 30 marks the row's last item.
+constexpr int PLAN_LAST = 1 << 30;
+__host__ __device__ inline int plan_item_w(int slot, bool last) { return (slot + 1) | (last ? PLAN_LAST : 0); }
+__host__ __device__ inline int plan_item_slot(int w) { return (w & (PLAN_LAST - 1)) - 1; }
+// plan header: [0] items, [1] split rows, [2] chunk, then the B, s_q and
+// max_kv_len it was built for
+constexpr int PLAN_HDR_B = 3, PLAN_HDR_SQ = 4, PLAN_HDR_MAXLEN = 5;
+
 // Physical cache row of logical position j of query (b, t); -1 if invalid.
 __device__ __forceinline__ int64_t resolve_row(const FwdParams& p, int b, int64_t jmax, int32_t j) {
     return dsa_rows::topk_row(j, jmax, p.block_table ? p.block_table + (int64_t)b * p.bt_stride : nullptr,
@@ -243,18 +252,31 @@ __device__ __forceinline__ void mfma_o(f32x16& acc, u32x4 a, u32x4 b) {
         asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 
-// bf16 pair -> fp16 pair.  Exact for |x| in [2^-14, 65504]; smaller values go
-// to fp16 subnormals (truncated, absolute error < 2^-24).
-__device__ __forceinline__ unsigned bf16x2_to_f16x2(unsigned w) {
-    const float lo = __uint_as_float(w << 16), hi = __uint_as_float(w & 0xFFFF0000u);
+// bf16 pair times s (a power of two) -> fp16 pair.  Exact for |x s| in
+// [2^-14, 65504]; smaller values go to fp16 subnormals (truncated, absolute
+// error < 2^-24).  s = 1 leaves every value as it is.
+__device__ __forceinline__ unsigned bf16x2_to_f16x2(unsigned w, float s) {
+    const float lo = __uint_as_float(w << 16) * s, hi = __uint_as_float(w & 0xFFFF0000u) * s;
     return __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(lo, hi));
 }
+// bf16 pair times s (a power of two) -> bf16 pair: exact unless a product
+// leaves bf16's normal range (|x s| < 2^-126).
+__device__ __forceinline__ unsigned bf16x2_scale(unsigned w, float s) {
+    const f32x2 v = {__uint_as_float(w << 16) * s, __uint_as_float(w & 0xFFFF0000u) * s};
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(v, bf16x2));
+}
+// fp16 range of the 656-B path.  Its K / V values are fp16(code * 2^e) *
+// fp16(mantissa) with scale = mantissa * 2^e, so every value of a row stays
+// below 448 * 128 = 57344 < 65504 when the row's scales are below 128.  A
+// scale of 128 or more, a negative or non-finite one (fp32 bits, unsigned,
+// >= those of 128.0) is outside the path's range: the query token's outputs
+// are then NaN, never a silently wrong attention.
+constexpr unsigned FP8_SCALE_LIMIT_BITS = 0x43000000u;   // 128.0f
 
 // 8 fp8 e4m3 codes (two dwords, low byte first) times 2^(e - 127) -> 8 bf16.
 // Exact: the scale is a power of two and bf16 has fp32's exponent range, so
 // every product is a bf16 value.  The scale operand is the fp32 2^(e - 127)
 // (its exponent field is e); v_cvt_scalef32_pk_bf16_fp8 applies it.
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u32x4 mx_to_bf16(unsigned c0, unsigned c1, unsigned e) {
     const float sf = __uint_as_float(e << 23);
     return u32x4{__builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)c0, sf, false)),
@@ -321,7 +343,31 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     int b = p.reverse ? (int)(gridDim.x / p.hgroups) - 1 - gx : gx, t = blockIdx.y;
     const int split = blockIdx.z;
     int item_k0 = 0, item_k1 = 0, item_slot = -1;
+    bool item_last = false;
     if (p.plan_items) {
+        // The plan must be the one built for this call's kv_indptr, B, s_q
+        // and max_kv_len.  A plan built for other arguments lays out other
+        // items and partial slots: then every query row's outputs are NaN,
+        // and nothing else is read or written.
+        const int32_t* hdr = p.plan_hdr;
+        if (__builtin_amdgcn_readfirstlane(hdr[PLAN_HDR_B]) != p.B ||
+            __builtin_amdgcn_readfirstlane(hdr[PLAN_HDR_SQ]) != p.s_q ||
+            __builtin_amdgcn_readfirstlane(hdr[PLAN_HDR_MAXLEN]) != p.chunk) {
+            // (the grid holds at least B * s_q workgroups per head group)
+            if (gx < p.B * p.s_q) {
+                const int bq = gx / p.s_q, tq = gx - bq * p.s_q;
+                __bf16* const orow = p.out + (int64_t)bq * p.o_sb + (int64_t)tq * p.o_st;
+                const unsigned nan2 = 0x7FC07FC0u;    // two bf16 NaNs
+                for (int i = (int)threadIdx.x; i < HEADS * (D_VO / 4); i += NTHR) {
+                    const int hh = hbase + i / (D_VO / 4);
+                    if (hh < p.H)
+                        reinterpret_cast<u32x2*>(orow + (int64_t)hh * p.o_sh)[i % (D_VO / 4)] = u32x2{nan2, nan2};
+                }
+                for (int hh = (int)threadIdx.x; hh < HEADS; hh += NTHR)
+                    if (p.lse && hbase + hh < p.H) p.lse[(int64_t)gx * p.H + hbase + hh] = __builtin_nanf("");
+            }
+            return;
+        }
         // Items are in row order, so the s_q rows of a batch (MTP tokens with
         // one list) are consecutive items.  Workgroups go to the 8 XCDs in
         // turn: within each group of 8 s_q workgroups, item s_q c + u runs on
@@ -337,11 +383,14 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         if (item >= __builtin_amdgcn_readfirstlane(p.plan_hdr[0])) return;
         const int4 w = p.plan_items[item];
         const int qrow_i = __builtin_amdgcn_readfirstlane(w.x);
+        if ((unsigned)qrow_i >= (unsigned)(p.B * p.s_q)) return;
         b = qrow_i / p.s_q;
         t = qrow_i - b * p.s_q;
         item_k0 = __builtin_amdgcn_readfirstlane(w.y);
         item_k1 = __builtin_amdgcn_readfirstlane(w.z);
-        item_slot = __builtin_amdgcn_readfirstlane(w.w);
+        const int ww = __builtin_amdgcn_readfirstlane(w.w);
+        item_slot = plan_item_slot(ww);
+        item_last = (ww & PLAN_LAST) != 0;
     }
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -351,7 +400,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // a copy of head H-1 and never stored.
     const int head_g = hbase + head;
     const int head_q = min(head_g, p.H - 1);
-    if (tid == 0) s_misc[4] = 0;
+    if (tid == 0) {
+        s_misc[4] = 0;    // restart flag
+        s_misc[5] = 0;    // 656-B rows: a scale outside the fp16 path's range was read
+    }
 
     // ---- 0. Q fragments (B operand of S^T = K Q^T): lane -> head r32, k-chunk hi ----
     // Issued first so their latency overlaps the index resolution below.
@@ -425,6 +477,9 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         const int64_t count = (int64_t)p.kv_indptr[b + 1] - kb - (p.s_q - 1 - t);
         k1 = (int)min(p.plan_items ? (int64_t)item_k1 : (int64_t)k0 + p.chunk, count);
         truncated = count > k_cap;
+        // a row's last item ends at the length the plan was built for: a list
+        // that has changed since is flagged (NaN), not silently cut
+        if (item_last && (int64_t)item_k1 != max(count, (int64_t)0)) truncated = true;
         idx = p.kv_indices + kb;
     } else {
         k1 = (int)min((int64_t)k0 + p.chunk, (int64_t)p.topk);
@@ -690,6 +745,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         }
         return d;
     };
+    // 656-B rows: set when a dequantised piece's scale is outside the fp16
+    // path's range (FP8_SCALE_LIMIT_BITS); range_bad collects it over the
+    // tiles that hold list rows.
+    bool deq_bad = false, range_bad = false;
     auto deq_store = [&](lds_ptr tb, int j, const DeqPiece& d) {
         const int ln = opaque(lane);
         if (j < TILE / NWAVE) {
@@ -705,6 +764,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                 return;
             }
             const float sc = __uint_as_float(d.v[2]);
+            deq_bad |= d.v[2] >= FP8_SCALE_LIMIT_BITS;
             const _Float16 m16 = (_Float16)__uint_as_float((d.v[2] & 0x007FFFFFu) | 0x3F800000u);
             const f16x2 mm = {m16, m16};
             const f16x2 h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)d.v[0], sc, false) * mm;
@@ -781,7 +841,9 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // happens (the maximum is exact), and none is allowed, so no input -
     // NaN, infinities or scores far beyond fp32's integer range included -
     // can keep the loop going.
-    const float c_s = p.scale_log2;
+    // (656-B rows: per head, times the power of two that brought its Q into
+    // fp16's range, see convert_q)
+    float c_s = p.scale_log2;
     // O^T accumulators of this wave: dims 128*wave + 32*m + (0..31) for the
     // 32 heads 32*h + (0..31): o[4*m + h] (the PV step is split by output
     // dims across the waves, so each gathered V value is read by one wave).
@@ -790,11 +852,32 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // Q conversion, once its loads have landed
     auto convert_q = [&]() {
         if constexpr (L::F16) {
-            // the NoPE part of Q is converted to fp16 for the fp16 MFMAs
+            // The NoPE part of Q is converted to fp16 for the fp16 MFMAs.  A
+            // head with |q| >= 2^15 would leave fp16's range: the whole head
+            // (NoPE and RoPE) is scaled by 2^-k, bringing its largest NoPE
+            // value below 2^15, and c_s by 2^k, so the scaled scores are the
+            // same.  Both are exact; k = 0 for every |q| < 2^15.
+            typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+            u16x2 amax = {0, 0};
 #pragma unroll
             for (int ks = 0; ks < KS_NOPE; ++ks)
 #pragma unroll
-                for (int w = 0; w < 4; ++w) qf[ks][w] = bf16x2_to_f16x2(qf[ks][w]);
+                for (int w = 0; w < 4; ++w)
+                    amax = __builtin_elementwise_max(amax, __builtin_bit_cast(u16x2, qf[ks][w] & 0x7FFF7FFFu));
+            // biased exponent of the head's largest |q| (bf16 bits >> 7)
+            int eb = max((int)amax[0], (int)amax[1]) >> 7;
+            eb = max(eb, __shfl_xor(eb, 32, 64));
+            const int k = max(eb - 141, 0);                   // 141 = 127 + 14
+            const float s = __uint_as_float((unsigned)(127 - k) << 23);
+            c_s = p.scale_log2 * __uint_as_float((unsigned)(127 + k) << 23);
+#pragma unroll
+            for (int ks = 0; ks < KS_NOPE; ++ks)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) qf[ks][w] = bf16x2_to_f16x2(qf[ks][w], s);
+#pragma unroll
+            for (int ks = KS_NOPE; ks < KS_ALL; ++ks)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) qf[ks][w] = bf16x2_scale(qf[ks][w], s);
         } else if constexpr (L::SQK) {
             // the codes stay fp8; the scale operands take, per lane, the bytes
             // of blocks 2 k8 + hi: the even (hi = 0) or odd bytes of the 16
@@ -944,6 +1027,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         const bool do_issue = it + NPRE < ntiles;
         const int issue_slot = FP8 ? it % 3 : (it + 2) % 3;
         const GatherRows gcur = gnext;
+        deq_bad = false;
         __builtin_amdgcn_sched_barrier(0);
         // Gathers of tile it+NPRE, all at once: the tile barrier just before
         // has drained this wave's LDS accesses, and an LDS-DMA load issued
@@ -1077,6 +1161,9 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             }
         }
         __builtin_amdgcn_sched_barrier(0);
+        // (past the last tile the dequant converted a stale slot: not counted)
+        if constexpr (L::F16)
+            if (it + 1 < ntiles) range_bad |= deq_bad;
     };
 
     // ---- bf16 caches: a software-pipelined tile loop ----
@@ -1284,7 +1371,9 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                     // tile 0 landed (tiles 1, 2 may still be in flight)
                     wait_tiles(min(ntiles, NPRE) - 1);
                     tile_barrier();
+                    deq_bad = false;
                     dequant(RING, T0);
+                    range_bad |= deq_bad;
                 }
                 // Two tiles per trip, so that the buffer being read and the one
                 // being filled are distinct LDS objects in each step.
@@ -1346,6 +1435,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         // per head: the largest score of the pass (log2 units); NaN compares false
         const float top = fmaxf(s_max, __shfl_xor(s_max, 32, 64)) * c_s;
         if (pass == 0 && __builtin_amdgcn_ballot_w64(top - m_ref > L::TAU) != 0 && lane == 0) s_misc[4] = 1;
+        if (L::F16 && range_bad) s_misc[5] = 1;
         tile_barrier();
         if (!s_misc[4]) break;
         // new reference: the exact maximum of every score of the head
@@ -1375,16 +1465,18 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     const int64_t part_row = p.plan_items ? (int64_t)item_slot : (int64_t)split * p.B * p.s_q + qrow;
     LDS_AS float* const s_l = (LDS_AS float*)PX;      // P buffer is free now
     // one tile: P is normalised.  A list longer than the caller's bound
-    // (max_kv_len / max_rows) was cut: its outputs are NaN, never a silently
-    // truncated attention.
-    if (hi == 0) s_l[head] = truncated ? __builtin_nanf("") : (has ? (nchunks == 1 && ntiles == 1 ? 1.0f : o_scale / l) : 0.0f);
+    // (max_kv_len / max_rows) was cut, or (656-B rows) a row's scale was
+    // outside the fp16 path's range: the outputs are NaN, never a silently
+    // truncated or wrong attention.
+    const bool nan_out = truncated || (L::F16 && s_misc[5] != 0);
+    if (hi == 0) s_l[head] = nan_out ? __builtin_nanf("") : (has ? (nchunks == 1 && ntiles == 1 ? 1.0f : o_scale / l) : 0.0f);
     if (hi == 0) {
-        const float lse_v = truncated ? __builtin_nanf("") : (m_fin + __builtin_amdgcn_logf(l)) * LN2;
+        const float lse_v = nan_out ? __builtin_nanf("") : (m_fin + __builtin_amdgcn_logf(l)) * LN2;
         if (head_g >= p.H) {
         } else if (!to_part) {
-            if (p.lse) p.lse[qrow * p.H + head_g] = has || truncated ? lse_v : INFINITY;
+            if (p.lse) p.lse[qrow * p.H + head_g] = has || nan_out ? lse_v : INFINITY;
         } else {
-            p.part_lse[part_row * p.H + head_g] = has || truncated ? lse_v : -FLT_MAX;
+            p.part_lse[part_row * p.H + head_g] = has || nan_out ? lse_v : -FLT_MAX;
         }
     }
     __syncthreads();
@@ -1499,7 +1591,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 // get_mla_metadata_kernel (opus_attn/dsa_v32/common/get_mla_metadata.hpp:
 // 8-158), which packs per-CU payloads serially; here equal-sized items are
 // left to the hardware dispatcher.
-// hdr[0] = items, hdr[1] = split rows, hdr[2] = chunk.
+// hdr[0] = items, hdr[1] = split rows, hdr[2] = chunk, hdr[3..5] = the B,
+// s_q and max_len the plan was built for (checked by the kernels that read
+// it).  Item counts per row are computed without int32 overflow for lists up
+// to DSA_MLA_MAX_LIST entries.
 // ---------------------------------------------------------------------------
 constexpr int PLAN_TARGET = 256;     // workgroups a plan aims at: one per CU
 constexpr int PLAN_MIN_CHUNK = 128;  // entries: at least four tiles per item
@@ -1552,7 +1647,7 @@ dsa_csr_plan_kernel(const int32_t* __restrict__ indptr, int B, int s_q, int max_
         int lo = PLAN_MIN_CHUNK / TILE, hi = max(lo, (lmax + TILE - 1) / TILE);   // in tiles
         while (lo < hi) {
             const int mid = (lo + hi) / 2, c = mid * TILE;
-            int n = tid < rows ? (Lr <= c ? 1 : (Lr + c - 1) / c) : 0;
+            int n = tid < rows ? (Lr <= c ? 1 : Lr / c + (Lr % c != 0)) : 0;
 #pragma unroll
             for (int off = 32; off >= 1; off >>= 1) n += __shfl_xor(n, off, 64);
             if (lane == 0) s_cnt[wave] = n;
@@ -1579,7 +1674,7 @@ dsa_csr_plan_kernel(const int32_t* __restrict__ indptr, int B, int s_q, int max_
         int L = 0, n = 0;
         if (q < rows) {
             L = few ? Lr : len_of(q);
-            n = L <= chunk ? 1 : (L + chunk - 1) / chunk;
+            n = L <= chunk ? 1 : L / chunk + (L % chunk != 0);
         }
         const int ns = n > 1 ? n : 0, sp = n > 1 ? 1 : 0;
         const int ia = wave_incl(n), ic = wave_incl(ns), id = wave_incl(sp);
@@ -1601,7 +1696,7 @@ dsa_csr_plan_kernel(const int32_t* __restrict__ indptr, int B, int s_q, int max_
         for (int j = 0; j < n; ++j) {
             const int e0 = L < 0 ? 0 : j * chunk;
             const int e1 = L < 0 ? 0 : (int)min((int64_t)(j + 1) * chunk, (int64_t)L);
-            items[ib + j] = make_int4(q, e0, e1, n > 1 ? sb + j : -1);
+            items[ib + j] = make_int4(q, e0, e1, plan_item_w(n > 1 ? sb + j : -1, j == n - 1));
         }
         if (n > 1) splits[pb] = make_int4(q, sb, n, 0);
         item_base += ta;
@@ -1613,6 +1708,9 @@ dsa_csr_plan_kernel(const int32_t* __restrict__ indptr, int B, int s_q, int max_
         hdr[0] = item_base;
         hdr[1] = split_base;
         hdr[2] = chunk;
+        hdr[PLAN_HDR_B] = B;
+        hdr[PLAN_HDR_SQ] = s_q;
+        hdr[PLAN_HDR_MAXLEN] = max_len;
     }
 }
 
@@ -1684,10 +1782,15 @@ dsa_mla_combine_kernel(const float* __restrict__ part_o, const float* __restrict
 // the hdr[1] x ceil(H / 4) units of four heads, so a plan without split rows
 // costs one wave of empty workgroups, not a workgroup per possible unit.
 __global__ void __launch_bounds__(256)
-dsa_mla_combine_plan_kernel(const float* __restrict__ part_o, const float* __restrict__ part_lse, int H,
-                            int s_q, __bf16* __restrict__ out, int64_t o_sb, int64_t o_st, int64_t o_sh,
-                            float* __restrict__ lse, const int4* __restrict__ map,
+dsa_mla_combine_plan_kernel(const float* __restrict__ part_o, const float* __restrict__ part_lse, int B, int H,
+                            int s_q, int max_len, __bf16* __restrict__ out, int64_t o_sb, int64_t o_st,
+                            int64_t o_sh, float* __restrict__ lse, const int4* __restrict__ map,
                             const int32_t* __restrict__ hdr) {
+    // a plan built for other arguments: the forward kernel has written NaN rows
+    if (__builtin_amdgcn_readfirstlane(hdr[PLAN_HDR_B]) != B ||
+        __builtin_amdgcn_readfirstlane(hdr[PLAN_HDR_SQ]) != s_q ||
+        __builtin_amdgcn_readfirstlane(hdr[PLAN_HDR_MAXLEN]) != max_len)
+        return;
     const int hq = (H + 3) / 4;
     const int units = __builtin_amdgcn_readfirstlane(hdr[1]) * hq;
     const int wave = threadIdx.x >> 6;
@@ -1939,8 +2042,8 @@ int csr_plan_launch(FwdParams& fp, int fmt, int max_len, void* ws, bool build, h
     const int r = launch_fwd(fp, fmt, (L.items_max + G - 1) / G * G, 1, 1, st);
     if (r || !L.slots_max) return r;
     hipLaunchKernelGGL(dsa_mla_combine_plan_kernel, dim3(4 * PLAN_TARGET), dim3(256), 0, st, (const float*)fp.part_o,
-                       (const float*)fp.part_lse, fp.H, fp.s_q, fp.out, fp.o_sb, fp.o_st, fp.o_sh, fp.lse,
-                       (const int4*)map, (const int32_t*)hdr);
+                       (const float*)fp.part_lse, fp.B, fp.H, fp.s_q, max_len, fp.out, fp.o_sb, fp.o_st, fp.o_sh,
+                       fp.lse, (const int4*)map, (const int32_t*)hdr);
     return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_HIP;
 }
 
@@ -2027,7 +2130,9 @@ const char* dsa_mla_strerror(int code) {
     case DSA_OK: return "success";
     case DSA_ERR_NULL_POINTER: return "a required pointer is NULL";
     case DSA_ERR_BAD_SHAPE: return "invalid shape argument";
-    case DSA_ERR_UNSUPPORTED: return "unsupported configuration (H must be 128; top-k per split <= 2048)";
+    case DSA_ERR_UNSUPPORTED:
+        return "unsupported configuration (V4 prefill head dim D other than 512, or an indexer head count "
+               "other than 32, 64 or 128)";
     case DSA_ERR_BAD_FORMAT: return "unknown kv_format";
     case DSA_ERR_WORKSPACE: return "workspace missing or too small";
     case DSA_ERR_BAD_SPLITS: return "num_splits out of range or too small for top-k";

@@ -169,6 +169,10 @@ def o_bound(ref: np.ndarray) -> np.ndarray:
 def assert_parity(o_got, lse_got, o_ref, lse_ref, what=""):
     g = oracle.bf16_to_f32(o_got)
     r = oracle.bf16_to_f32(o_ref)
+    # O is a convex mix of finite V rows: a NaN or infinity on either side is a mismatch
+    # (the comparisons below are False for NaN, so they would let it pass)
+    assert np.isfinite(r).all(), f"{what}: the reference O holds {int((~np.isfinite(r)).sum())} non-finite values"
+    assert np.isfinite(g).all(), f"{what}: O holds {int((~np.isfinite(g)).sum())} non-finite values"
     e_o = o_max_abs(o_got, o_ref)
     e_l = lse_rel(lse_got, lse_ref)
     if g.size and not np.isnan(g).any():

@@ -199,8 +199,10 @@ def test_csr_plan_invariants(dev):
     torch.cuda.synchronize()
     assert (bits(out2) == bits(out)).all()
     w = ws.cpu().numpy()
-    hdr = w[:12].view(np.int32)
-    n_items, n_split, chunk = (int(x) for x in hdr)
+    hdr = w[:24].view(np.int32)
+    n_items, n_split, chunk, h_b, h_sq, h_max = (int(x) for x in hdr)
+    # the arguments the plan was built for (checked by the kernels that read it)
+    assert (h_b, h_sq, h_max) == (len(lens), s_q, max(lens))
     L = [max(0, lens[q_ // s_q] - (s_q - 1 - q_ % s_q)) for q_ in range(rows)]
     # fewer than 256 rows: the smallest chunk (in tiles, >= 128) whose items fit 256
     def n_of(c):
@@ -209,7 +211,10 @@ def test_csr_plan_invariants(dev):
     while n_of(want) > 256:
         want += 32
     assert chunk == want and n_items == n_of(chunk) <= 256
-    items = w[256:256 + 16 * n_items].view(np.int32).reshape(n_items, 4)
+    items = w[256:256 + 16 * n_items].view(np.int32).reshape(n_items, 4).copy()
+    # field w: the partial slot + 1 in bits 0..29, bit 30 on a row's last item
+    last = (items[:, 3] >> 30) & 1
+    items[:, 3] = (items[:, 3] & ((1 << 30) - 1)) - 1
     items_max = rows + 256
     map_off = (256 + 16 * items_max + 255) // 256 * 256
     smap = w[map_off:map_off + 16 * n_split].view(np.int32).reshape(n_split, 4)
@@ -217,6 +222,7 @@ def test_csr_plan_invariants(dev):
     for r in range(rows):
         n = 1 if L[r] <= chunk else -(-L[r] // chunk)
         mine = items[pos:pos + n]
+        assert list(last[pos:pos + n]) == [0] * (n - 1) + [1]
         pos += n
         assert (mine[:, 0] == r).all()
         if n == 1:
@@ -252,3 +258,46 @@ def test_csr_plan_reuse(dev, fp8):
         assert np.array_equal(l_pl.cpu().numpy(), l_own.cpu().numpy())
     o_ref, l_ref = oracle_csr(q2, kv, indptr, indices, s_q)
     assert_parity(bits(o_pl), l_pl.cpu().numpy(), o_ref, l_ref, "csr planned")
+
+
+def test_csr_plan_mismatch_is_nan(dev):
+    """A reused plan (DSA_MLA_SPLITS_PLANNED) built for other arguments is detected, not
+    trusted: B, s_q and max_kv_len are checked against the plan's header (every query row
+    of the call gets NaN O and LSE, and nothing is read or written out of place), and a
+    row whose list has changed length since planning gets NaN (its last item no longer
+    ends at the row's length) while the other rows stay exact."""
+    lens, s_q = [5_000, 17, 0, 1_200], 2
+    q, kv, indptr, indices = csr_case(97, lens, s_q, 8_000)
+    ip, ix = torch.from_numpy(indptr).to(dev), torch.from_numpy(indices).to(dev)
+    # one workspace, larger than any of the calls below needs, holds the plan throughout
+    big = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    ws = dsa.csr_plan(ip, len(lens), s_q, 128, max(lens), workspace=big)
+    # (1) max_kv_len differs from the plan's: every row NaN
+    out, lse = dsa.mla_decode_csr(t16(q, dev), t16(kv, dev), ip, ix, SM_SCALE, s_q=s_q,
+                                  max_kv_len=max(lens) + 64, num_splits=abi.SPLITS_PLANNED,
+                                  workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all() and torch.isnan(lse).all()
+    # (2) B differs (the first three batches of the same lists): every row NaN
+    ws = dsa.csr_plan(ip, len(lens), s_q, 128, max(lens), workspace=big)
+    q3 = q[:3 * s_q]
+    out, lse = dsa.mla_decode_csr(t16(q3, dev), t16(kv, dev), ip[:4], ix, SM_SCALE, s_q=s_q,
+                                  max_kv_len=max(lens), num_splits=abi.SPLITS_PLANNED,
+                                  workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all() and torch.isnan(lse).all()
+    # (3) a list grown and one shrunk since planning: those rows NaN, the rest exact
+    ws = dsa.csr_plan(ip, len(lens), s_q, 128, max(lens), workspace=big)
+    lens2 = [4_000, 17, 0, 1_300]
+    q2, kv2, indptr2, indices2 = csr_case(98, lens2, s_q, 8_000)
+    ip2, ix2 = torch.from_numpy(indptr2).to(dev), torch.from_numpy(indices2).to(dev)
+    out, lse = dsa.mla_decode_csr(t16(q2, dev), t16(kv2, dev), ip2, ix2, SM_SCALE, s_q=s_q,
+                                  max_kv_len=max(lens), num_splits=abi.SPLITS_PLANNED,
+                                  workspace=ws)
+    torch.cuda.synchronize()
+    o_ref, l_ref = oracle_csr(q2, kv2, indptr2, indices2, s_q)
+    lse = lse.cpu().numpy()
+    changed = np.repeat(np.array(lens2) != np.array(lens), s_q)
+    assert np.isnan(lse[changed]).all() and torch.isnan(out[torch.from_numpy(changed)].float()).all()
+    keep = ~changed
+    assert_parity(bits(out)[keep], lse[keep], o_ref[keep], l_ref[keep], "csr stale plan: unchanged rows")

@@ -301,3 +301,18 @@ def test_thread_count_does_not_change_results():
     o1, l1 = c.oracle(num_threads=1)
     o2, l2 = c.oracle(num_threads=5)
     assert np.array_equal(o1, o2) and np.array_equal(l1, l2)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_power_of_two_query_scale_is_exact(fp8):
+    """q * 2^k with sm_scale * 2^-k gives bit-identical O and LSE: the scores (q . k) * sm_scale
+    are the same fp32 values.  The GPU's 656-B path relies on exactly this to bring a head
+    with |q| >= 2^15 into fp16's range; here q reaches about 2^16 * 3, past fp16's 65504."""
+    c = small_decode(31, fp8=fp8)
+    o1, l1 = c.oracle()
+    k = 16
+    q2 = oracle.bf16_bits(oracle.bf16_to_f32(c.q) * np.float32(2.0 ** k))
+    assert np.abs(oracle.bf16_to_f32(q2)).max() > 6.5e4
+    o2, l2 = oracle.mla_decode(q2, c.kv, c.indices, c.seq_lens, np.float32(c.sm_scale * 2.0 ** -k),
+                               block_table=c.block_table, block_size=c.block_size, causal=c.causal)
+    assert np.array_equal(o1, o2) and np.array_equal(l1, l2)

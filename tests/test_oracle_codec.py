@@ -112,6 +112,12 @@ def test_row_656_layout_and_roundtrip():
     rng = np.random.default_rng(3)
     src = oracle.bf16_to_f32(oracle.normal_bf16(rng, (64, 576)))
     src[5, 128:256] = 0.0                      # all-zero group -> scale 0, codes 0
+    # rows far outside N(0,1): a whole row times 2^15 (amax ~1e5) and one group with a
+    # -1e5 entry (scale ~223, above the GPU fp16 path's limit of 128): the oracle's codec
+    # and dequant hold the same bound there (the reference dequantises in fp32,
+    # opus_attn/dsa_v32/common/host.cc:418-429)
+    src[9] *= np.float32(2.0 ** 15)
+    src[10, 3 * 128 + 9] = oracle.bf16_to_f32(oracle.bf16_bits(np.array([-1.0e5], np.float32)))[0]
     rows = oracle.quantize_rows_656(src)
     assert rows.shape == (64, 656)
     scales = rows[:, 512:528].copy().view(np.float32)
@@ -141,6 +147,7 @@ def test_row_656_layout_and_roundtrip():
     err = np.abs(deq[:, :512].reshape(64, 4, 128).astype(np.float64)
                  - src[:, :512].reshape(64, 4, 128).astype(np.float64))
     assert (err <= bound + 1e-30).all()
+    assert scales[10, 3] > 128.0 and np.abs(deq[10, 3 * 128 + 9] + 1.0e5) <= 1.0e5 * 2.0 ** -4
 
 
 @pytest.mark.parametrize("v", [0.0, 1.0, -3.5, 448.0])

@@ -50,3 +50,12 @@ def test_lse_bar():
     assert_parity(o, np.array([10.0 + 0.0109, 0.00099], np.float32), o, ref, "lse ok")
     with pytest.raises(AssertionError):
         assert_parity(o, np.array([10.0 + 0.0111, 0.0], np.float32), o, ref, "lse off")
+
+
+@pytest.mark.parametrize("ref_v,got_v", [(float("nan"), 1.0),        # NaN in the reference
+                                          (1.0, float("nan")),        # NaN in the result
+                                          (float("inf"), 3.0e38)])    # inf reference, finite result
+def test_assert_parity_rejects_non_finite(ref_v, got_v):
+    lse = np.zeros(1, np.float32)
+    with pytest.raises(AssertionError):
+        assert_parity(_o([got_v, 0.5]), lse, _o([ref_v, 0.5]), lse, "non-finite")
