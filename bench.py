@@ -62,6 +62,10 @@ CONFIGS = {
     # queries, 1024 scattered prefix rows of 65536 pages plus a 128-row extend window, D=512
     "v4": dict(kind="v4", N=4096, topk=1024, pages=65536, window=128, fp8=False),
     "v4fp8": dict(kind="v4", N=4096, topk=1024, pages=65536, window=128, fp8=True),
+    # split-K prefill: the harness at -n 16 -topk 0 (every one of 65536 pages, scattered, plus the
+    # 128-row window): 16 queries would leave 240 of 256 CUs idle unsplit
+    "v4split": dict(kind="v4", N=16, topk=65536, pages=65536, window=128, fp8=False),
+    "v4fp8split": dict(kind="v4", N=16, topk=65536, pages=65536, window=128, fp8=True),
     # top-k index selection producing the c3 step's lists: 256 query tokens (B=128, s_q=2),
     # causal lengths n - s_q + j + 1; five score sets (320 MB) alternate, above the 256 MB MALL
     "topk": dict(kind="topk", T=256, n=65536, s_q=2, topk=2048, sets=5),
@@ -83,6 +87,8 @@ NAMES = {
     "v4": "DeepSeek-V4 bf16 prefill N=4096 H=128 D=512, top-k 1024 of 65536 pages + window 128, sink",
     "v4fp8": ("DeepSeek-V4 fp8 prefill (448 e4m3 + 14 E8M0 | 64 bf16) N=4096 H=128, top-k 1024 of "
               "65536 pages + window 128, sink"),
+    "v4split": "DeepSeek-V4 bf16 prefill N=16 H=128 D=512, -topk 0 (all 65536 pages) + window 128, sink",
+    "v4fp8split": "DeepSeek-V4 fp8 prefill N=16 H=128, -topk 0 (all 65536 pages) + window 128, sink",
     "topk": ("top-k index selection for the c3 step: 256 query tokens (B=128 s_q=2), fp32 scores, "
              "causal lengths up to 65536, top-k 2048 (5 score sets alternate step by step)"),
     "csr_skew": ("bf16 CSR decode on the reference's --varlen lists: B=8, lengths U[5, 131072], "
@@ -94,6 +100,24 @@ NAMES = {
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# CPU baselines run after every GPU timing (see main): (message, leg dict, job)
+CPU_JOBS = []
+
+
+def defer_cpu(args, msg, leg, job):
+    """Queue leg["cpu_baseline"] = job() for after the GPU legs and the headline, so that no
+    GPU leg starts on a GPU left idle by seconds of CPU work."""
+    if not args.no_cpu:
+        CPU_JOBS.append((msg, leg, job))
+
+
+def run_cpu_jobs():
+    for msg, leg, job in CPU_JOBS:
+        log(msg)
+        leg["cpu_baseline"] = job()
+    CPU_JOBS.clear()
 
 
 # ------------------------------------------------------------------ inputs
@@ -337,8 +361,9 @@ def make_v4(cfg, dev, seed=2051):
                 rows=N * topk + int(ne.sum()), N=N)
 
 
-def v4_step(v, dev):
-    """(step, buffers) for one V4 prefill call through the C ABI (arguments built once)."""
+def v4_step(v, dev, splits=0):
+    """(step, buffers) for one V4 prefill call through the C ABI (arguments built once), with
+    num_splits = splits (0 = the library's automatic choice) and its workspace."""
     import ctypes
     import torch
     from opfoundry_amd import abi
@@ -372,14 +397,19 @@ def v4_step(v, dev):
     a.kv_indptr_extend, a.kv_indices_extend = ipe.data_ptr(), ide.data_ptr()
     a.N, a.H, a.max_rows = N, H, mr
     a.softmax_scale = 1.0 / math.sqrt(512.0)
+    a.num_splits = splits
     ap = ctypes.byref(a)
     st = torch.cuda.current_stream().cuda_stream
+    n = ctypes.c_size_t(0)
+    check(getattr(load_library(), name + "_workspace_size")(ap, ctypes.byref(n)), name + "_workspace_size")
+    ws = torch.empty(max(n.value, 16), dtype=torch.uint8, device=dev)
+    wp, wb = ws.data_ptr(), n.value
 
     def step():
-        rc = fn(ap, st)
+        rc = fn(ap, wp, wb, st)
         if rc:
             check(rc, name)
-    return step, (out, lse, a)
+    return step, (out, lse, a, ws)
 
 
 def cpu_baseline_v4(v, sample):
@@ -640,12 +670,13 @@ def graph_replay(make_step, calls):
     return g.replay, g
 
 
-def decode_leg(name, args, dev):
-    """One decode configuration (c1, c2, c4) as a leg of the JSON line: step time, the fused
-    kernel's roofline, the reference's own figures and the CPU oracle on the same inputs.  c1
-    and c4 (a few microseconds per step) are timed as HIP-graph replays of 20 steps; c2 as
-    stream launches like the headline.  Unsplit, the step is the fused kernel; c4's step also
-    holds the combine kernel, and its roofline is taken over the whole step."""
+def decode_leg(name, args, dev, dst):
+    """One decode configuration (c1, c2, c4) as a leg of the JSON line (dst[name]): step time,
+    the fused kernel's roofline, the reference's own figures and the CPU oracle on the same
+    inputs.  c1 and c4 (a few microseconds per step) are timed as HIP-graph replays of 20
+    steps; c2 as stream launches like the headline.  Unsplit, the step is the fused kernel;
+    c4's step also holds the combine kernel, and its roofline is taken over the whole step.
+    A generator: inputs are built up to the yield, the timing follows."""
     import torch
     from opfoundry_amd import dsa
     cfg = CONFIGS[name]
@@ -663,6 +694,8 @@ def decode_leg(name, args, dev):
     if graphed:
         calls = 20
         replay, g = graph_replay(lambda: prepared_decode(a, ws), calls)
+    yield
+    if graphed:
         reps = max(5, args.steps // 4)
         ms = time_steps(replay, reps, args.warmup) / calls
         timing = f"HIP graph of {calls} steps, replayed {reps} times"
@@ -690,12 +723,9 @@ def decode_leg(name, args, dev):
                         "mfma_frac": round(FLOP_PER_PAIR * V / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)},
            "reference_figures": reference_figures(T, s_q, V, row_bytes, ms)}
     del g, a, ws, out, lse
-    if not args.no_cpu:
-        log(f"CPU baseline (oracle) on {name}")
-        leg["cpu_baseline"] = cpu_baseline_decode(d, cfg["fp8"], min(args.cpu_sample, 64), T)
-    del d
-    torch.cuda.empty_cache()
-    return leg
+    defer_cpu(args, f"CPU baseline (oracle) on {name}", leg,
+              lambda: cpu_baseline_decode(d, cfg["fp8"], min(args.cpu_sample, 64), T))
+    dst[name] = leg
 
 
 def make_csr_skew(cfg, dev, seed=2071):
@@ -717,7 +747,7 @@ def make_csr_skew(cfg, dev, seed=2071):
     return dict(q=q, kv=kv, indptr=indptr, indices=indices, lens=lens.cpu().tolist(), s_q=s_q, total=total)
 
 
-def csr_skew_leg(args, dev):
+def csr_skew_leg(args, dev, dst):
     """The skewed CSR batch through the device work plan (built once, reused by the timed
     calls) and through uniform splits (32 per row: the 256 workgroups the per-row rule gives 8
     rows), timed as stream launches in three alternating rounds (the median of each), with
@@ -755,6 +785,7 @@ def csr_skew_leg(args, dev):
         torch.cuda.synchronize()
         outs[name] = (out.clone(), lse.clone())
         steps[name] = (step, ws, a)
+    yield
     # a comparison: three alternating rounds, the median of each
     times = {name: [] for name in steps}
     for _ in range(3):
@@ -781,7 +812,7 @@ def csr_skew_leg(args, dev):
            "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
                         "kernel": "dsa_mla_fwd_kernel<bf16> + dsa_mla_combine_plan_kernel (whole step)", "kernel_avg_us": round(ms * 1e3, 3), "alg_bytes": alg}}
-    if not args.no_cpu:
+    def cpu():
         # the oracle on the first 16384 entries of the longest list, scaled to every entry
         import oracle
         b = int(np.argmax(c["lens"]))
@@ -795,13 +826,13 @@ def csr_skew_leg(args, dev):
         t0 = time.perf_counter()
         oracle.mla_decode(q, kv, idx, np.full(1, n, np.int32), SM_SCALE, num_threads=nt)
         dt = time.perf_counter() - t0
-        leg["cpu_baseline"] = dict(value=dt * V / n * 1e6, unit="us/step", cores=1, kind="port",
-                                   cpu_model=cpu_model(),
-                                   sample=f"{n} entries of one row ({dt:.2f} s; one row is one oracle task), "
-                                          f"scaled x{V / n:.1f} to the step's {V} entries")
-    del c, out, lse
-    torch.cuda.empty_cache()
-    return leg
+        return dict(value=dt * V / n * 1e6, unit="us/step", cores=1, kind="port",
+                    cpu_model=cpu_model(),
+                    sample=f"{n} entries of one row ({dt:.2f} s; one row is one oracle task), "
+                           f"scaled x{V / n:.1f} to the step's {V} entries")
+    defer_cpu(args, "CPU baseline (oracle) on csr_skew", leg, cpu)
+    del out, lse
+    dst["csr_skew"] = leg
 
 
 def make_indexer(cfg, dev, seed=2081):
@@ -821,7 +852,7 @@ def make_indexer(cfg, dev, seed=2081):
     return dict(q=q, w=w, k=k, bt=bt, sl=sl, scores=scores, bs=bs, seq=seq)
 
 
-def indexer_leg(args, dev):
+def indexer_leg(args, dev, dst):
     """The index scorer on the c3 step's shape: step time, HBM roofline (k rows read once per
     sequence, scores written), MFMA share, and numpy's float64 oracle on a sample."""
     import ctypes
@@ -847,6 +878,7 @@ def indexer_leg(args, dev):
         rc = fn(ap, st)
         if rc:
             check(rc, "dsa_indexer_scores")
+    yield
     ms = time_steps(step, args.steps, args.warmup)
     pairs = sum(seq - (s_q - 1 - t) for t in range(s_q)) * B        # (token, position) pairs
     alg = B * seq * 256 + pairs * 4 + x["q"].numel() * 2 + x["w"].numel() * 4
@@ -858,7 +890,7 @@ def indexer_leg(args, dev):
                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": profiled_traffic("dsa_indexer_traffic.txt"),
                         "kernel": "dsa_indexer_kernel<64>", "kernel_avg_us": round(ms * 1e3, 3), "alg_bytes": alg,
                         "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}}
-    if not args.no_cpu:
+    def cpu():
         import oracle
         try:
             from threadpoolctl import threadpool_info
@@ -873,13 +905,12 @@ def indexer_leg(args, dev):
         t0 = time.perf_counter()
         oracle.indexer_scores(qn, wn, kn, x["sl"][:nb].cpu().numpy(), k_batch_stride=seq, causal=True, n_cols=seq)
         dt = time.perf_counter() - t0
-        leg["cpu_baseline"] = dict(value=dt * B / nb * 1e6, unit="us/step", cores=nt, kind="port",
-                                   cpu_model=cpu_model(),
-                                   sample=f"{nb} of {B} sequences (both tokens, all positions; float64 numpy, "
-                                          f"{nt} BLAS threads), {dt:.2f} s, scaled x{B / nb:.0f}")
-    del x
-    torch.cuda.empty_cache()
-    return leg
+        return dict(value=dt * B / nb * 1e6, unit="us/step", cores=nt, kind="port",
+                    cpu_model=cpu_model(),
+                    sample=f"{nb} of {B} sequences (both tokens, all positions; float64 numpy, "
+                           f"{nt} BLAS threads), {dt:.2f} s, scaled x{B / nb:.0f}")
+    defer_cpu(args, "CPU baseline (numpy float64 oracle) on the indexer", leg, cpu)
+    dst["indexer"] = leg
 
 
 # -------------------------------------------------------------- CPU baseline
@@ -1010,8 +1041,10 @@ def main():
         if not args.kernel_only:
             ap.error("--config indexer is reported inside the default JSON line; use it with --kernel-only")
         args.no_cpu = True
-        leg = indexer_leg(args, dev)
-        print(json.dumps({"config": args.config, "ms_per_step": leg["us_per_step"] / 1e3}))
+        out = {}
+        for _ in indexer_leg(args, dev, out):
+            pass
+        print(json.dumps({"config": args.config, "ms_per_step": out["indexer"]["us_per_step"] / 1e3}))
         return
     if cfg["kind"] == "topk":
         if not args.kernel_only:
@@ -1063,9 +1096,8 @@ def main():
     res = {}
     legs_before_headline(args, dev, res)
 
-    # The headline is timed right after the last GPU leg (the c5 prefill), before any CPU
-    # baseline: its W warm-up steps then start on a GPU whose clocks have settled under
-    # sustained load.  From a cold start (or after ~2 s idle) the first ~100 c3 steps run
+    # The headline is timed right after the other legs, before any CPU baseline: its W
+    # warm-up steps then start on a GPU whose clocks have settled under sustained load.  From a cold start (or after ~2 s idle) the first ~100 c3 steps run
     # up to 30 % slower while the GPU's power management settles, whatever the kernel.
     log(f"timing {args.steps} steps after warm-up (splits={ns})")
     n_warm = warm_up(step, args.warmup)
@@ -1112,14 +1144,10 @@ def main():
     del out, lse, ws, step, a
     res.update(legs)
     res["reference_figures"] = reference_figures(B * s_q, s_q, V, row_bytes, ms)
-    if not args.no_cpu:
-        log("CPU baseline (oracle) on a bounded sample")
-        res["cpu_baseline"] = cpu_baseline_decode(d, cfg["fp8"], args.cpu_sample, B * s_q)
-        if "prefill" in res:
-            res["prefill"]["cpu_baseline"] = cpu_baseline_prefill(legs.pop("_c5"), args.cpu_prefill_sample,
-                                                                  res["prefill"]["valid_pairs"])
-    legs.pop("_c5", None)
-    res.pop("_c5", None)
+    # every CPU baseline, after all GPU timing
+    defer_cpu(args, "CPU baseline (oracle) on a bounded sample of the headline", res,
+              lambda: cpu_baseline_decode(d, cfg["fp8"], args.cpu_sample, B * s_q))
+    run_cpu_jobs()
     del d
     torch.cuda.empty_cache()
     if not args.no_peaks:
@@ -1131,122 +1159,169 @@ def main():
 
 
 def legs_before_headline(args, dev, res):
-    """Every leg but the headline, into res: decode legs, csr_skew, indexer, mx, the V4
-    prefills, top-k, and last the c5 prefill (its CPU baseline runs after the headline; its
-    inputs are left in res["_c5"])."""
+    """Every leg but the headline, into res: the decode legs, csr_skew, top-k, the indexer, the
+    V4 prefills (split-K rows first), mx and the c5 prefill.  Each leg is a generator that
+    builds its inputs up to a yield: every input is built first, then the legs are timed back
+    to back, so no leg starts on a GPU left idle by input generation or CPU work.  The CPU
+    baselines are queued (defer_cpu) and run after the headline."""
     import torch
+    gens = []
+    # order: light legs first, the MFMA-heavy ones last and c5 right before the headline.  A
+    # change from light to heavy load costs ~20 ms of lower clocks while the GPU's power
+    # management settles (the first ~100 c3 steps after a light leg run up to 30 % slower);
+    # heavy after heavy does not.
     if not args.no_legs:
         res["decode_legs"] = {}
-        for name in ("c1", "c2", "c4"):
+        for name in ("c1", "c4", "c2"):
             if name != args.config:
-                log(f"decode leg {name}")
-                res["decode_legs"][name] = decode_leg(name, args, dev)
-        log("csr_skew leg (device work plan against uniform splits)")
-        res["csr_skew"] = csr_skew_leg(args, dev)
-        log("indexer leg")
-        res["indexer"] = indexer_leg(args, dev)
-
-    if not args.no_mx:
-        log("building mx (MXFP8 split-stream) inputs")
-        m = make_mx(CONFIGS["mx"], dev)
-        mstep, keep, mplan = mx_step(m, dev)
-        mms = time_steps(mstep, args.steps, args.warmup)   # warm-up as the decode leg
-        plan_ms = time_steps(mplan, args.steps, args.warmup)
-        mk_ms = None
-        del keep
-        T = m["q"][0].shape[0]
-        L = m["L"]
-        mV = sum(L - (m["s_q"] - 1 - t) for t in range(m["s_q"])) * (T // m["s_q"])
-        # both tokens of an MTP pair share their batch's list: each row counts once
-        nb = T // m["s_q"]
-        m_bytes = T * H * (512 + 16 + 128) + nb * L * (656 + 4) + T * H * D_VO * 2 + T * H * 4
-        mdom = mk_ms if mk_ms is not None else mms
-        mach = m_bytes / (mdom * 1e-3) / 1e9
-        res["mxfp8"] = {"workload": f"mx: {NAMES['mx']}", "us_per_step": round(mms * 1e3, 3),
-                        "plan": "CSR work plan built once and reused (num_splits = DSA_MLA_SPLITS_PLANNED), "
-                                "as the reference times its decode after get_mla_metadata",
-                        "plan_us": round(plan_ms * 1e3, 3),
-                        "dtype": "MXFP8 (e4m3 + E8M0) KV and Q -> exact bf16 dequant, bf16 MFMA, f32 accumulate",
-                        "valid_pairs": mV, "hbm_TBps": round(m_bytes / (mms * 1e-3) / 1e12, 3),
-                        "roofline": {"bound": "hbm", "achieved": round(mach, 1), "peak": HBM_PEAK_GBS,
-                                     "unit": "GB/s", "frac": round(mach / HBM_PEAK_GBS, 4),
-                                     "traffic": profiled_traffic("dsa_mla_fwd_mxfp8_mx_traffic.txt"),
-                                     "kernel": "dsa_mla_fwd_kernel<mxfp8>",
-                                     "kernel_avg_us": round(mdom * 1e3, 3), "alg_bytes": m_bytes,
-                                     "mfma_frac": round(FLOP_PER_PAIR * mV / (mdom * 1e-3) / 1e12
-                                                        / BF16_PEAK_TFLOPS, 4)}}
-        if not args.no_cpu:
-            log("CPU baseline (oracle) on an MXFP8 sample")
-            res["mxfp8"]["cpu_baseline"] = cpu_baseline_mx(m, args.cpu_mx_sample)
-        del m
-        torch.cuda.empty_cache()
-
+                gens.append((f"decode leg {name}", decode_leg(name, args, dev, res["decode_legs"])))
+        gens.append(("csr_skew leg (device work plan against uniform splits)", csr_skew_leg(args, dev, res)))
+    if not args.no_topk:
+        gens.append(("topk leg", topk_leg(args, dev, res)))
+    if not args.no_legs:
+        gens.append(("indexer leg", indexer_leg(args, dev, res)))
     if not args.no_v4:
         res["v4_prefill"] = {}
+        for name in ("v4split", "v4fp8split"):
+            gens.append((f"{name} leg (split-K against unsplit)", v4_split_leg(name, args, dev, res["v4_prefill"])))
         for name in ("v4", "v4fp8"):
-            log(f"building {name} inputs")
-            v = make_v4(CONFIGS[name], dev)
-            vstep, keep = v4_step(v, dev)
-            vsteps = max(5, args.steps // 5)
-            vms = time_steps(vstep, vsteps, args.warmup)    # one kernel per step
-            vfl = 4.0 * H * v["rows"] * 512                   # the reference's count (mla_v4_host.cc:358)
-            leg = {"workload": f"{name}: {NAMES[name]}", "ms_per_step": round(vms, 4),
-                   "tflops": round(vfl / (vms * 1e-3) / 1e12, 1), "rows": v["rows"],
-                   "roofline": {"bound": "mfma", "achieved": round(vfl / (vms * 1e-3) / 1e12, 1),
-                                "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                "frac": round(vfl / (vms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
-                                "traffic": profiled_traffic(f"dsa_mla_fwd_{name}_traffic.txt"),
-                                "kernel": "dsa_mla_fwd_kernel<mxfp8_v4>" if v["fp8"] else "dsa_mla_fwd_kernel<bf16_d512>",
-                                "kernel_avg_us": round(vms * 1e3, 1)}}
-            del keep
-            if not args.no_cpu:
-                log(f"CPU baseline (oracle) on a {name} sample")
-                leg["cpu_baseline"] = cpu_baseline_v4(v, args.cpu_v4_sample)
-            res["v4_prefill"][name] = leg
-            del v, vstep
-            torch.cuda.empty_cache()
-
-    if not args.no_topk:
-        log("building topk inputs")
-        tk = make_topk(CONFIGS["topk"], dev)
-        tstep = topk_step(tk)
-        tms = time_steps(tstep, args.steps, args.warmup)
-        tk_ms = tms       # one kernel per step: the timed region's average launch
-        t_bytes = 4 * int(tk["lengths"].sum().item()) + 4 * tk["T"] * tk["topk"]
-        tach = t_bytes / (tk_ms * 1e-3) / 1e9
-        res["topk"] = {"workload": f"topk: {NAMES['topk']}", "us_per_step": round(tms * 1e3, 3),
-                       "dtype": "fp32 scores -> int32 positions",
-                       "roofline": {"bound": "hbm", "achieved": round(tach, 1), "peak": HBM_PEAK_GBS,
-                                    "unit": "GB/s", "frac": round(tach / HBM_PEAK_GBS, 4),
-                                    "traffic": profiled_traffic("dsa_topk_traffic.txt"),
-                                    "kernel": "dsa_topk_reg_kernel", "kernel_avg_us": round(tk_ms * 1e3, 3),
-                                    "alg_bytes": t_bytes}}
-        if not args.no_cpu:
-            log("CPU baseline (oracle) on a topk sample")
-            res["topk"]["cpu_baseline"] = cpu_baseline_topk(tk, args.cpu_topk_sample)
-        del tk, tstep
-        torch.cuda.empty_cache()
-
+            gens.append((f"{name} leg", v4_leg(name, args, dev, res["v4_prefill"])))
+    if not args.no_mx:
+        gens.append(("mx (MXFP8 split-stream) leg", mx_leg(args, dev, res)))
     if not args.no_prefill:
-        log("building c5 prefill inputs")
-        p = make_prefill(CONFIGS["c5"], dev)
-        pstep, keep = prefill_step(p, dev)
-        psteps = max(3, args.steps // 5)
-        pms = time_steps(pstep, psteps, args.warmup)
-        pk_ms = pms       # one kernel per step: the timed region's average launch
-        del keep
-        pV = int((p["idx"] >= 0).sum())
-        pfl = FLOP_PER_PAIR * pV
-        res["prefill"] = {"workload": f"c5: {NAMES['c5']}", "ms_per_step": round(pms, 4),
-                          "tflops": round(pfl / (pms * 1e-3) / 1e12, 1), "valid_pairs": pV,
-                          "roofline": {"bound": "mfma", "achieved": round(pfl / (pk_ms * 1e-3) / 1e12, 1),
-                                       "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                       "frac": round(pfl / (pk_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
-                                       "traffic": profiled_traffic("dsa_mla_fwd_bf16_c5_traffic.txt"),
-                                       "kernel": "dsa_mla_fwd_kernel<bf16>",
-                                       "kernel_avg_us": round(pk_ms * 1e3, 1)}}
-        if not args.no_cpu:
-            res["_c5"] = p     # CPU baseline after the headline
+        gens.append(("c5 prefill", c5_leg(args, dev, res)))
+    for msg, g in gens:
+        log(f"building inputs: {msg}")
+        next(g)
+    torch.cuda.synchronize()
+    for msg, g in gens:
+        log(f"timing: {msg}")
+        for _ in g:
+            pass
+
+
+def c5_leg(args, dev, res):
+    p = make_prefill(CONFIGS["c5"], dev)
+    pstep, keep = prefill_step(p, dev)
+    psteps = max(3, args.steps // 5)
+    yield
+    pms = time_steps(pstep, psteps, args.warmup)
+    pk_ms = pms       # one kernel per step: the timed region's average launch
+    del keep
+    pV = int((p["idx"] >= 0).sum())
+    pfl = FLOP_PER_PAIR * pV
+    res["prefill"] = {"workload": f"c5: {NAMES['c5']}", "ms_per_step": round(pms, 4),
+                      "tflops": round(pfl / (pms * 1e-3) / 1e12, 1), "valid_pairs": pV,
+                      "roofline": {"bound": "mfma", "achieved": round(pfl / (pk_ms * 1e-3) / 1e12, 1),
+                                   "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                   "frac": round(pfl / (pk_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                                   "traffic": profiled_traffic("dsa_mla_fwd_bf16_c5_traffic.txt"),
+                                   "kernel": "dsa_mla_fwd_kernel<bf16>",
+                                   "kernel_avg_us": round(pk_ms * 1e3, 1)}}
+    defer_cpu(args, "CPU baseline (oracle) on a c5 sample", res["prefill"],
+              lambda: cpu_baseline_prefill(p, args.cpu_prefill_sample, pV))
+
+
+def mx_leg(args, dev, res):
+    m = make_mx(CONFIGS["mx"], dev)
+    mstep, keep, mplan = mx_step(m, dev)
+    yield
+    mms = time_steps(mstep, args.steps, args.warmup)   # warm-up as the decode leg
+    plan_ms = time_steps(mplan, args.steps, args.warmup)
+    del keep
+    T = m["q"][0].shape[0]
+    L = m["L"]
+    mV = sum(L - (m["s_q"] - 1 - t) for t in range(m["s_q"])) * (T // m["s_q"])
+    # both tokens of an MTP pair share their batch's list: each row counts once
+    nb = T // m["s_q"]
+    m_bytes = T * H * (512 + 16 + 128) + nb * L * (656 + 4) + T * H * D_VO * 2 + T * H * 4
+    mach = m_bytes / (mms * 1e-3) / 1e9
+    res["mxfp8"] = {"workload": f"mx: {NAMES['mx']}", "us_per_step": round(mms * 1e3, 3),
+                    "plan": "CSR work plan built once and reused (num_splits = DSA_MLA_SPLITS_PLANNED), "
+                            "as the reference times its decode after get_mla_metadata",
+                    "plan_us": round(plan_ms * 1e3, 3),
+                    "dtype": "MXFP8 (e4m3 + E8M0) KV and Q -> exact bf16 dequant, bf16 MFMA, f32 accumulate",
+                    "valid_pairs": mV, "hbm_TBps": round(m_bytes / (mms * 1e-3) / 1e12, 3),
+                    "roofline": {"bound": "hbm", "achieved": round(mach, 1), "peak": HBM_PEAK_GBS,
+                                 "unit": "GB/s", "frac": round(mach / HBM_PEAK_GBS, 4),
+                                 "traffic": profiled_traffic("dsa_mla_fwd_mxfp8_mx_traffic.txt"),
+                                 "kernel": "dsa_mla_fwd_kernel<mxfp8>",
+                                 "kernel_avg_us": round(mms * 1e3, 3), "alg_bytes": m_bytes,
+                                 "mfma_frac": round(FLOP_PER_PAIR * mV / (mms * 1e-3) / 1e12
+                                                    / BF16_PEAK_TFLOPS, 4)}}
+    defer_cpu(args, "CPU baseline (oracle) on an MXFP8 sample", res["mxfp8"],
+              lambda: cpu_baseline_mx(m, args.cpu_mx_sample))
+
+
+def v4_leg(name, args, dev, dst):
+    v = make_v4(CONFIGS[name], dev)
+    vstep, keep = v4_step(v, dev)
+    vsteps = max(5, args.steps // 5)
+    yield
+    vms = time_steps(vstep, vsteps, args.warmup)    # one kernel per step
+    vfl = 4.0 * H * v["rows"] * 512                   # the reference's count (mla_v4_host.cc:358)
+    leg = {"workload": f"{name}: {NAMES[name]}", "ms_per_step": round(vms, 4),
+           "tflops": round(vfl / (vms * 1e-3) / 1e12, 1), "rows": v["rows"],
+           "roofline": {"bound": "mfma", "achieved": round(vfl / (vms * 1e-3) / 1e12, 1),
+                        "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(vfl / (vms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                        "traffic": profiled_traffic(f"dsa_mla_fwd_{name}_traffic.txt"),
+                        "kernel": "dsa_mla_fwd_kernel<mxfp8_v4>" if v["fp8"] else "dsa_mla_fwd_kernel<bf16_d512>",
+                        "kernel_avg_us": round(vms * 1e3, 1)}}
+    del keep
+    defer_cpu(args, f"CPU baseline (oracle) on a {name} sample", leg,
+              lambda: cpu_baseline_v4(v, args.cpu_v4_sample))
+    dst[name] = leg
+
+
+def v4_split_leg(name, args, dev, dst):
+    """Split-K: few queries with long lists (the harness at -n 16 -topk 0), the automatic split
+    count against one workgroup per query, in three alternating rounds (the median of each)."""
+    import torch
+    v = make_v4(CONFIGS[name], dev)
+    runs = {"split": v4_step(v, dev, 0), "unsplit": v4_step(v, dev, 1)}
+    ws = runs["split"][1][3]
+    ns = (ws.numel() - 256) // (v["N"] * H * 513 * 4) if ws.numel() > 16 else 1
+    vsteps = max(5, args.steps // 5)
+    yield
+    times = {k: [] for k in runs}
+    for _ in range(3):
+        for k, (st_, _) in runs.items():
+            times[k].append(time_steps(st_, vsteps, args.warmup))
+    t = {k: sorted(x)[1] for k, x in times.items()}
+    torch.cuda.synchronize()
+    d_o = (runs["split"][1][0].float() - runs["unsplit"][1][0].float()).abs().max().item()
+    vfl = 4.0 * H * v["rows"] * 512
+    tf = vfl / (t["split"] * 1e-3) / 1e12
+    dst[name] = {
+        "workload": f"{name}: {NAMES[name]}", "num_splits": ns, "rows": v["rows"],
+        "ms_per_step": round(t["split"], 4), "unsplit_ms_per_step": round(t["unsplit"], 4),
+        "split_speedup": round(t["unsplit"] / t["split"], 2), "split_vs_unsplit_max_abs_dO": d_o,
+        "tflops": round(tf, 1),
+        "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": ("dsa_mla_fwd_kernel<mxfp8_v4>" if v["fp8"] else "dsa_mla_fwd_kernel<bf16_d512>")
+                               + " + dsa_mla_combine_kernel (whole step)",
+                     "kernel_avg_us": round(t["split"] * 1e3, 1)}}
+
+
+def topk_leg(args, dev, res):
+    tk = make_topk(CONFIGS["topk"], dev)
+    tstep = topk_step(tk)
+    yield
+    tms = time_steps(tstep, args.steps, args.warmup)
+    tk_ms = tms       # one kernel per step: the timed region's average launch
+    t_bytes = 4 * int(tk["lengths"].sum().item()) + 4 * tk["T"] * tk["topk"]
+    tach = t_bytes / (tk_ms * 1e-3) / 1e9
+    res["topk"] = {"workload": f"topk: {NAMES['topk']}", "us_per_step": round(tms * 1e3, 3),
+                   "dtype": "fp32 scores -> int32 positions",
+                   "roofline": {"bound": "hbm", "achieved": round(tach, 1), "peak": HBM_PEAK_GBS,
+                                "unit": "GB/s", "frac": round(tach / HBM_PEAK_GBS, 4),
+                                "traffic": profiled_traffic("dsa_topk_traffic.txt"),
+                                "kernel": "dsa_topk_reg_kernel", "kernel_avg_us": round(tk_ms * 1e3, 3),
+                                "alg_bytes": t_bytes}}
+    defer_cpu(args, "CPU baseline (oracle) on a topk sample", res["topk"],
+              lambda: cpu_baseline_topk(tk, args.cpu_topk_sample))
 
 
 if __name__ == "__main__":

@@ -346,6 +346,14 @@ int dsa_mla_decode_mxfp8(const dsa_mla_decode_mxfp8_args* args, void* workspace,
  *           valid iff 0 <= j < kv_rows and, when causal != 0,
  *           j <= i + causal_offset
  * out     : bf16 [N, H, 512]; lse fp32 [N, H] (may be NULL)
+ * num_splits: split-K over each query's list (the reference's split layout,
+ *           opus_attn/dsa_v4/common/mla_prefill_split.h:7-54): 0 = automatic
+ *           (more than one only when fewer than 256 workgroups, N x
+ *           ceil(H / 128), would run; at least 256 list entries per split);
+ *           1..DSA_MLA_MAX_SPLITS: each query's list cut into num_splits
+ *           contiguous parts whose fp32 partials (O and LSE, in the
+ *           workspace: num_splits x N x H x 513 floats) a combine kernel
+ *           merges.  Unsplit calls need no workspace.
  * Replaces mla_v4_prefill_launch, opus_attn/dsa_v4/common/mla_v4_host.cc:28-47,
  * with the V3.2 shape (576 / 512), no attention sink, and an LSE output.
  */
@@ -365,8 +373,10 @@ typedef struct {
     int32_t causal;
     int64_t causal_offset;
     float sm_scale;
+    int32_t num_splits;          /* 0 = automatic */
 } dsa_mla_prefill_args;
 
+/* Workspace bytes dsa_mla_prefill needs (0 when it runs unsplit). */
 int dsa_mla_prefill_workspace_size(const dsa_mla_prefill_args* args, size_t* bytes);
 int dsa_mla_prefill(const dsa_mla_prefill_args* args, void* workspace, size_t workspace_bytes,
                     void* stream);
@@ -387,8 +397,17 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* args, void* workspace, size_t wo
  * reference, may be NULL) is the natural log of the denominator, sink
  * included.  max_rows bounds the prefix + extend entries of any query (a
  * query with more gets NaN O and LSE, never a silently truncated attention);
- * a list of any length runs in the query's one workgroup, 2048 entries at a
+ * a list of any length runs in one workgroup per split, 2048 entries at a
  * time.  total_pages and total_tokens must be below 2^30.
+ * num_splits: split-K over each query's prefix-then-extend list, as the
+ * reference's split prefill cuts it (opus_attn/dsa_v4/common/mla_prefill_split.h:
+ * 34-44: part s of whole 32-row tiles, prefix rows first): 0 = automatic
+ * (more than one only when fewer than 256 workgroups, N x ceil(H / 128),
+ * would run, keeping at least 256 entries of max_rows per split); else
+ * 1..DSA_MLA_MAX_SPLITS.  The splits write fp32 partials (O and LSE, no sink;
+ * workspace num_splits x N x H x 513 floats, from
+ * dsa_mla_prefill_v4_workspace_size) and a combine kernel merges them with
+ * the sink joining the denominator once (mla_v4_host.cc:469-472).
  */
 typedef struct {
     const void* q;
@@ -407,9 +426,13 @@ typedef struct {
     int32_t stride_kv_page;
     int32_t max_rows;
     float softmax_scale;
+    int32_t num_splits;          /* 0 = automatic (an addition to the reference kargs) */
 } dsa_mla_prefill_v4_args;
 
-int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* args, void* stream);
+/* Workspace bytes dsa_mla_prefill_v4 needs (0 when it runs unsplit). */
+int dsa_mla_prefill_v4_workspace_size(const dsa_mla_prefill_v4_args* args, size_t* bytes);
+int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* args, void* workspace, size_t workspace_bytes,
+                       void* stream);
 
 /*
  * DeepSeek-V4 sparse prefill on fp8 rows: the argument set of
@@ -423,7 +446,7 @@ int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* args, void* stream);
  * Value d < 448 = float(e4m3(code_d)) * 2^(scale[d / 32] - 127); values
  * 448..511 are the RoPE values (decode_dsa_row_fp8, mla_v4_host.cc:443-453).
  * K = V = the 512-value row; softmax, sink, pools, CSR lists, skipping and
- * LSE exactly as in dsa_mla_prefill_v4.  Strides in elements of each stream
+ * LSE, num_splits and the workspace exactly as in dsa_mla_prefill_v4.  Strides in elements of each stream
  * (bytes for nope, bf16 elements for rope and out); nope pointers and strides
  * 16-byte aligned, rope strides multiples of 8, out strides of 4.  The kernel
  * never reads the pad bytes, nor any row the lists do not name.
@@ -450,9 +473,13 @@ typedef struct {
     int32_t stride_kv_nope_page, stride_kv_rope_page;
     int32_t max_rows;
     float softmax_scale;
+    int32_t num_splits;          /* 0 = automatic (an addition to the reference kargs) */
 } dsa_mla_prefill_v4_fp8_args;
 
-int dsa_mla_prefill_v4_fp8(const dsa_mla_prefill_v4_fp8_args* args, void* stream);
+/* Workspace bytes dsa_mla_prefill_v4_fp8 needs (0 when it runs unsplit). */
+int dsa_mla_prefill_v4_fp8_workspace_size(const dsa_mla_prefill_v4_fp8_args* args, size_t* bytes);
+int dsa_mla_prefill_v4_fp8(const dsa_mla_prefill_v4_fp8_args* args, void* workspace, size_t workspace_bytes,
+                           void* stream);
 
 /*
  * fp8 cache writer: quantise n_rows bf16 latent rows (576 values, row stride

@@ -54,7 +54,9 @@ EXPORTED_SYMBOLS = (
     "dsa_mla_combine",
     "dsa_mla_prefill_workspace_size",
     "dsa_mla_prefill",
+    "dsa_mla_prefill_v4_workspace_size",
     "dsa_mla_prefill_v4",
+    "dsa_mla_prefill_v4_fp8_workspace_size",
     "dsa_mla_prefill_v4_fp8",
     "dsa_kv_quantize_fp8",
     "dsa_topk_indices",
@@ -63,7 +65,7 @@ EXPORTED_SYMBOLS = (
     "dsa_mla_abi_version",
 )
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -130,7 +132,7 @@ class PrefillArgs(ctypes.Structure):
         ("out", _vp), ("o_stride_n", _i64), ("o_stride_h", _i64),
         ("lse", _vp),
         ("N", _i32), ("H", _i32), ("topk", _i32), ("causal", _i32),
-        ("causal_offset", _i64), ("sm_scale", ctypes.c_float),
+        ("causal_offset", _i64), ("sm_scale", ctypes.c_float), ("num_splits", _i32),
     ]
 
 
@@ -143,7 +145,7 @@ class PrefillV4Args(ctypes.Structure):
         ("kv_indptr_extend", _vp), ("kv_indices_extend", _vp),
         ("N", _i32), ("H", _i32), ("D", _i32), ("total_pages", _i32), ("total_tokens", _i32),
         ("stride_qo_n", _i32), ("stride_qo_h", _i32), ("stride_kv_page", _i32), ("max_rows", _i32),
-        ("softmax_scale", ctypes.c_float),
+        ("softmax_scale", ctypes.c_float), ("num_splits", _i32),
     ]
 
 
@@ -162,7 +164,7 @@ class PrefillV4Fp8Args(ctypes.Structure):
         ("stride_q_rope_n", _i32), ("stride_q_rope_h", _i32),
         ("stride_o_n", _i32), ("stride_o_h", _i32),
         ("stride_kv_nope_page", _i32), ("stride_kv_rope_page", _i32),
-        ("max_rows", _i32), ("softmax_scale", ctypes.c_float),
+        ("max_rows", _i32), ("softmax_scale", ctypes.c_float), ("num_splits", _i32),
     ]
 
 
@@ -215,8 +217,10 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
     lib.dsa_mla_combine.argtypes = [_vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _vp, _vp]
     lib.dsa_mla_prefill_workspace_size.argtypes = [ctypes.POINTER(PrefillArgs), sz]
     lib.dsa_mla_prefill.argtypes = [ctypes.POINTER(PrefillArgs), _vp, ctypes.c_size_t, _vp]
-    lib.dsa_mla_prefill_v4.argtypes = [ctypes.POINTER(PrefillV4Args), _vp]
-    lib.dsa_mla_prefill_v4_fp8.argtypes = [ctypes.POINTER(PrefillV4Fp8Args), _vp]
+    lib.dsa_mla_prefill_v4_workspace_size.argtypes = [ctypes.POINTER(PrefillV4Args), sz]
+    lib.dsa_mla_prefill_v4.argtypes = [ctypes.POINTER(PrefillV4Args), _vp, ctypes.c_size_t, _vp]
+    lib.dsa_mla_prefill_v4_fp8_workspace_size.argtypes = [ctypes.POINTER(PrefillV4Fp8Args), sz]
+    lib.dsa_mla_prefill_v4_fp8.argtypes = [ctypes.POINTER(PrefillV4Fp8Args), _vp, ctypes.c_size_t, _vp]
     lib.dsa_kv_quantize_fp8.argtypes = [_vp, _i64, _i64, _vp, _i64, _vp, _vp]
     lib.dsa_topk_indices.argtypes = [_vp, _i64, _vp, _i32, _i32, _i32, _vp, _i64, _vp]
     lib.dsa_mla_strerror.argtypes = [ctypes.c_int]

@@ -454,7 +454,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // (s_q - 1 - t), the reference's count-based MTP causality
     // (opus_attn/dsa_v32/common/host.cc:524-526); a row outside the cache is
     // skipped.
-    const int k0 = p.plan_items ? item_k0 : split * p.chunk;
+    int k0 = p.plan_items ? item_k0 : split * p.chunk;
     int k1;
     int64_t jmax = 0;
     const int32_t* idx;
@@ -469,8 +469,16 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         v4_np = max((int64_t)p.ind_pre[b + 1] - pb, (int64_t)0);
         v4_eb = p.ind_ext[b];
         const int64_t ne = max((int64_t)p.ind_ext[b + 1] - v4_eb, (int64_t)0);
-        k1 = (int)min((int64_t)k0 + p.chunk, v4_np + ne);
-        truncated = v4_np + ne > k_cap;
+        // the token's list (at most max_rows = p.topk entries: a longer one is
+        // cut, NaN) split into gridDim.z parts of whole tiles, as the
+        // reference's split-K prefill cuts prefix-then-extend rows
+        // (opus_attn/dsa_v4/common/mla_prefill_split.h:34-44)
+        const int64_t n_b = min(v4_np + ne, (int64_t)p.topk);
+        truncated = v4_np + ne > p.topk;
+        const int64_t per = (n_b + gridDim.z - 1) / gridDim.z;
+        const int64_t cb = (per + TILE - 1) / TILE * TILE;
+        k0 = (int)min((int64_t)split * cb, n_b);
+        k1 = (int)min((int64_t)k0 + cb, n_b);
         idx = p.idx_pre + pb;
     } else if (p.kv_indptr) {
         const int64_t kb = p.kv_indptr[b];
@@ -1715,11 +1723,17 @@ dsa_csr_plan_kernel(const int32_t* __restrict__ indptr, int B, int s_q, int max_
 }
 
 // One (query row, head) of a combine, on one wave: ns partial rows, split s
-// at partial row first + s * step_rows.
+// at partial row first + s * step_rows.  sink (V4 prefill, per head, natural
+// log units, or NULL): an attention sink joins the denominator once, here,
+// as in the reference's split fold (the splits themselves run without it):
+// m = max(lse_i, sink), den = sum w_i + exp(sink - m), so a sink far above
+// or below every score neither overflows nor underflows.  A row with no
+// attended entry keeps O = 0 and LSE = +inf, as unsplit.
 __device__ __forceinline__ void combine_head(const float* __restrict__ part_o, const float* __restrict__ part_lse,
                                              int ns, int64_t first, int64_t step_rows, int row, int head, int H,
                                              int s_q, __bf16* __restrict__ out, int64_t o_sb, int64_t o_st,
-                                             int64_t o_sh, float* __restrict__ lse, int lane) {
+                                             int64_t o_sh, float* __restrict__ lse, const float* __restrict__ sink,
+                                             int lane) {
     const int64_t stride = step_rows * H;
     const int64_t base = first * H + head;     // partial index of split 0
     const int64_t rh = (int64_t)row * H + head;
@@ -1727,6 +1741,9 @@ __device__ __forceinline__ void combine_head(const float* __restrict__ part_o, c
     for (int s = lane; s < ns; s += 64) m = fmaxf(m, part_lse[s * stride + base]);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    const bool sink_on = sink != nullptr && m > -FLT_MAX;
+    const float sk = sink_on ? sink[head] : 0.0f;
+    if (sink_on) m = fmaxf(m, sk);
     f32x4 acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
     float den = 0.0f;
     // eight splits' loads in flight at a time; sums in split order
@@ -1754,8 +1771,8 @@ __device__ __forceinline__ void combine_head(const float* __restrict__ part_o, c
             }
         }
     }
+    if (sink_on) den += __builtin_amdgcn_exp2f((sk - m) * LOG2E);
     const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
     const bf16x4 b0 = __builtin_convertvector(acc0 * inv, bf16x4);
     const bf16x4 b1 = __builtin_convertvector(acc1 * inv, bf16x4);
     __bf16* op = out + (int64_t)(row / s_q) * o_sb + (int64_t)(row % s_q) * o_st + (int64_t)head * o_sh + 8 * lane;
@@ -1769,11 +1786,11 @@ __device__ __forceinline__ void combine_head(const float* __restrict__ part_o, c
 __global__ void __launch_bounds__(256)
 dsa_mla_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_lse, int ns,
                        int rows, int H, int s_q, __bf16* __restrict__ out, int64_t o_sb, int64_t o_st,
-                       int64_t o_sh, float* __restrict__ lse) {
+                       int64_t o_sh, float* __restrict__ lse, const float* __restrict__ sink) {
     const int row = blockIdx.x;
     const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
     if (head >= H) return;
-    combine_head(part_o, part_lse, ns, row, rows, row, head, H, s_q, out, o_sb, o_st, o_sh, lse,
+    combine_head(part_o, part_lse, ns, row, rows, row, head, H, s_q, out, o_sb, o_st, o_sh, lse, sink,
                  threadIdx.x & 63);
 }
 
@@ -1799,7 +1816,7 @@ dsa_mla_combine_plan_kernel(const float* __restrict__ part_o, const float* __res
         const int head = (u - r * hq) * 4 + wave;
         if (head < H) {
             const int4 m = map[r];
-            combine_head(part_o, part_lse, m.z, m.y, 1, m.x, head, H, s_q, out, o_sb, o_st, o_sh, lse,
+            combine_head(part_o, part_lse, m.z, m.y, 1, m.x, head, H, s_q, out, o_sb, o_st, o_sh, lse, nullptr,
                          threadIdx.x & 63);
         }
     }
@@ -1976,11 +1993,11 @@ int launch_fwd(const FwdParams& fp, int fmt, int B, int s_q, int ns, hipStream_t
 }
 
 int launch_combine(const float* po, const float* pl, int ns, int rows, int H, int s_q, void* out, int64_t o_sb,
-                   int64_t o_st, int64_t o_sh, float* lse, hipStream_t st) {
+                   int64_t o_st, int64_t o_sh, float* lse, hipStream_t st, const float* sink = nullptr) {
     if (rows == 0) return DSA_OK;
     dim3 grid(rows, (H + 3) / 4), block(256);
     hipLaunchKernelGGL(dsa_mla_combine_kernel, grid, block, 0, st, po, pl, ns, rows, H, s_q, (__bf16*)out, o_sb,
-                       o_st, o_sh, lse);
+                       o_st, o_sh, lse, sink);
     return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_HIP;
 }
 
@@ -2119,11 +2136,114 @@ size_t mx_ws_bytes(const dsa_mla_decode_mxfp8_args* a, int ns) {
     return ns == 1 ? 0 : (size_t)ns * a->B * a->s_q * a->H * (D_VO + 1) * sizeof(float) + 256;
 }
 
+// Splits of a prefill: num_splits when given, else (0) more than one only when
+// fewer than 256 workgroups (query tokens x head groups) would run, keeping at
+// least 8 tiles (256 entries of the longest list) per split.  A token's
+// split s covers its list's part s of whole tiles; the partials are merged by
+// the combine kernel (with the attention sink, V4).
+int prefill_splits(int requested, int64_t wgs, int64_t max_list) {
+    if (requested > 0) return requested;
+    if (wgs <= 0 || wgs >= 256) return 1;
+    const int64_t want = (256 + wgs - 1) / wgs;
+    const int64_t by_len = std::max<int64_t>(1, max_list / 256);
+    return (int)std::min<int64_t>(std::min<int64_t>(want, by_len), DSA_MLA_MAX_SPLITS);
+}
+size_t prefill_ws_bytes(int ns, int64_t N, int H) {
+    return ns <= 1 || N == 0 ? 0 : (size_t)ns * N * H * (D_VO + 1) * sizeof(float) + 256;
+}
+// Forward kernel over ns splits of N query tokens, then (ns > 1) the combine of
+// their partials, with the attention sink folded in once by the combine.
+int prefill_launch(FwdParams& fp, int fmt, int ns, const float* sink, void* ws, hipStream_t st) {
+    const int64_t N = fp.B;
+    if (ns > 1) {
+        fp.part_o = (float*)ws;
+        fp.part_lse = (float*)((char*)ws + (size_t)ns * N * fp.H * D_VO * sizeof(float));
+        fp.attn_sink = nullptr;
+    } else {
+        fp.attn_sink = sink;
+    }
+    const int r = launch_fwd(fp, fmt, (int)N, 1, ns, st);
+    if (r || ns == 1) return r;
+    return launch_combine(fp.part_o, fp.part_lse, ns, (int)N, fp.H, 1, fp.out, fp.o_sb, 0, fp.o_sh, fp.lse, st,
+                          sink);
+}
+
+int validate_prefill(const dsa_mla_prefill_args* a, int* ns_out) {
+    if (!a) return DSA_ERR_NULL_POINTER;
+    if (a->N < 0 || a->topk < 0 || a->kv_rows < 0 || a->kv_rows > INT32_MAX) return DSA_ERR_BAD_SHAPE;
+    if (!heads_ok(a->H, a->N)) return DSA_ERR_BAD_SHAPE;
+    if (a->kv_format != DSA_KV_BF16 && a->kv_format != DSA_KV_FP8_656) return DSA_ERR_BAD_FORMAT;
+    if (row_stride_bytes(a->kv_format, a->kv_stride_row) < 0) return DSA_ERR_BAD_STRIDE;
+    if (a->topk > MAX_LIST) return DSA_ERR_BAD_SHAPE;
+    if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
+    *ns_out = prefill_splits(a->num_splits, (int64_t)a->N * head_groups(a->H), a->topk);
+    if (a->N == 0) return DSA_OK;
+    if (!a->q || !a->out || (a->topk > 0 && (!a->kv || !a->indices))) return DSA_ERR_NULL_POINTER;
+    if ((a->q_stride_n % 8) || (a->q_stride_h % 8) || (a->o_stride_n % 4) || (a->o_stride_h % 4))
+        return DSA_ERR_BAD_STRIDE;
+    if (((uintptr_t)a->q & 15) || ((uintptr_t)a->kv & 15) || ((uintptr_t)a->out & 7)) return DSA_ERR_BAD_STRIDE;
+    return DSA_OK;
+}
+
+int validate_v4(const dsa_mla_prefill_v4_args* a, int* ns_out) {
+    if (!a) return DSA_ERR_NULL_POINTER;
+    if (a->N < 0 || a->total_pages < 0 || a->total_tokens < 0 || a->max_rows < 0) return DSA_ERR_BAD_SHAPE;
+    // row ids carry their pool in bit 30 (dsa_rows.h): each pool stays below 2^30 rows
+    if (a->total_pages >= dsa_rows::MAX_POOL_ROWS || a->total_tokens >= dsa_rows::MAX_POOL_ROWS)
+        return DSA_ERR_BAD_SHAPE;
+    if (a->max_rows > MAX_LIST) return DSA_ERR_BAD_SHAPE;
+    if (!heads_ok(a->H, a->N)) return DSA_ERR_BAD_SHAPE;
+    if (a->D != DSA_MLA_D_V4) return DSA_ERR_UNSUPPORTED;
+    if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
+    *ns_out = prefill_splits(a->num_splits, (int64_t)a->N * head_groups(a->H), a->max_rows);
+    if (a->N == 0) return DSA_OK;
+    if (!a->q || !a->out || !a->kv_indptr_prefix || !a->kv_indices_prefix || !a->kv_indptr_extend ||
+        !a->kv_indices_extend)
+        return DSA_ERR_NULL_POINTER;
+    if ((a->total_pages > 0 && !a->unified_kv) || (a->total_tokens > 0 && !a->kv)) return DSA_ERR_NULL_POINTER;
+    if (a->stride_qo_n < 0 || a->stride_qo_h < 0 || (a->stride_qo_n % 8) || (a->stride_qo_h % 8) ||
+        a->stride_kv_page < DSA_MLA_D_V4 || (a->stride_kv_page % 8))
+        return DSA_ERR_BAD_STRIDE;
+    if (((uintptr_t)a->q & 15) || ((uintptr_t)a->unified_kv & 15) || ((uintptr_t)a->kv & 15) ||
+        ((uintptr_t)a->out & 7))
+        return DSA_ERR_BAD_STRIDE;
+    return DSA_OK;
+}
+
+int validate_v4fp8(const dsa_mla_prefill_v4_fp8_args* a, int* ns_out) {
+    if (!a) return DSA_ERR_NULL_POINTER;
+    if (a->N < 0 || a->total_pages < 0 || a->total_tokens < 0 || a->max_rows < 0) return DSA_ERR_BAD_SHAPE;
+    if (a->total_pages >= dsa_rows::MAX_POOL_ROWS || a->total_tokens >= dsa_rows::MAX_POOL_ROWS)
+        return DSA_ERR_BAD_SHAPE;
+    if (a->max_rows > MAX_LIST) return DSA_ERR_BAD_SHAPE;
+    if (!heads_ok(a->H, a->N)) return DSA_ERR_BAD_SHAPE;
+    if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
+    *ns_out = prefill_splits(a->num_splits, (int64_t)a->N * head_groups(a->H), a->max_rows);
+    if (a->N == 0) return DSA_OK;
+    if (!a->q_nope || !a->q_rope || !a->out || !a->kv_indptr_prefix || !a->kv_indices_prefix ||
+        !a->kv_indptr_extend || !a->kv_indices_extend)
+        return DSA_ERR_NULL_POINTER;
+    if ((a->total_pages > 0 && (!a->unified_kv_nope || !a->unified_kv_rope)) ||
+        (a->total_tokens > 0 && (!a->kv_nope || !a->kv_rope)))
+        return DSA_ERR_NULL_POINTER;
+    const int32_t b16[] = {a->stride_q_nope_n, a->stride_q_nope_h, a->stride_kv_nope_page};
+    for (int32_t v : b16) if (v < 0 || (v % 16)) return DSA_ERR_BAD_STRIDE;
+    if (a->stride_kv_nope_page < DSA_MLA_V4_NOPE_BYTES) return DSA_ERR_BAD_STRIDE;
+    const int32_t e8[] = {a->stride_q_rope_n, a->stride_q_rope_h, a->stride_kv_rope_page};
+    for (int32_t v : e8) if (v < 0 || (v % 8)) return DSA_ERR_BAD_STRIDE;
+    if (a->stride_o_n < 0 || a->stride_o_h < 0 || (a->stride_o_n % 4) || (a->stride_o_h % 4))
+        return DSA_ERR_BAD_STRIDE;
+    const void* ptrs[] = {a->q_nope, a->q_rope, a->unified_kv_nope, a->unified_kv_rope, a->kv_nope, a->kv_rope};
+    for (const void* q : ptrs) if ((uintptr_t)q & 15) return DSA_ERR_BAD_STRIDE;
+    if ((uintptr_t)a->out & 7) return DSA_ERR_BAD_STRIDE;
+    return DSA_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
-int dsa_mla_abi_version(void) { return 7; }
+int dsa_mla_abi_version(void) { return 8; }
 
 const char* dsa_mla_strerror(int code) {
     switch (code) {
@@ -2351,27 +2471,21 @@ int dsa_mla_combine(const float* po, const float* pl, int32_t ns, int32_t rows, 
 }
 
 int dsa_mla_prefill_workspace_size(const dsa_mla_prefill_args* a, size_t* bytes) {
-    if (!a || !bytes) return DSA_ERR_NULL_POINTER;
-    if (a->N < 0 || a->topk < 0 || a->kv_rows < 0) return DSA_ERR_BAD_SHAPE;
-    if (!heads_ok(a->H, a->N)) return DSA_ERR_BAD_SHAPE;
-    if (a->topk > MAX_LIST) return DSA_ERR_BAD_SHAPE;
-    *bytes = 0;
+    if (!bytes) return DSA_ERR_NULL_POINTER;
+    int ns;
+    const int rc = validate_prefill(a, &ns);
+    if (rc) return rc;
+    *bytes = prefill_ws_bytes(ns, a->N, a->H);
     return DSA_OK;
 }
 
 int dsa_mla_prefill(const dsa_mla_prefill_args* a, void* ws, size_t ws_bytes, void* stream) {
-    (void)ws; (void)ws_bytes;
-    if (!a) return DSA_ERR_NULL_POINTER;
-    if (a->N < 0 || a->topk < 0 || a->kv_rows < 0 || a->kv_rows > INT32_MAX) return DSA_ERR_BAD_SHAPE;
-    if (!heads_ok(a->H, a->N)) return DSA_ERR_BAD_SHAPE;
-    if (a->kv_format != DSA_KV_BF16 && a->kv_format != DSA_KV_FP8_656) return DSA_ERR_BAD_FORMAT;
-    if (row_stride_bytes(a->kv_format, a->kv_stride_row) < 0) return DSA_ERR_BAD_STRIDE;
-    if (a->topk > MAX_LIST) return DSA_ERR_BAD_SHAPE;
+    int ns;
+    const int rc = validate_prefill(a, &ns);
+    if (rc) return rc;
+    const size_t need = prefill_ws_bytes(ns, a->N, a->H);
+    if (need && (!ws || ws_bytes < need || ((uintptr_t)ws & 15))) return DSA_ERR_WORKSPACE;
     if (a->N == 0) return DSA_OK;
-    if (!a->q || !a->out || (a->topk > 0 && (!a->kv || !a->indices))) return DSA_ERR_NULL_POINTER;
-    if ((a->q_stride_n % 8) || (a->q_stride_h % 8) || (a->o_stride_n % 4) || (a->o_stride_h % 4))
-        return DSA_ERR_BAD_STRIDE;
-    if (((uintptr_t)a->q & 15) || ((uintptr_t)a->kv & 15) || ((uintptr_t)a->out & 7)) return DSA_ERR_BAD_STRIDE;
     FwdParams fp{};
     fp.H = a->H;
     fp.hgroups = head_groups(a->H);
@@ -2391,34 +2505,31 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* a, void* ws, size_t ws_bytes, vo
     fp.out = (__bf16*)a->out;
     fp.o_sb = a->o_stride_n; fp.o_st = 0; fp.o_sh = a->o_stride_h;
     fp.lse = a->lse;
-    fp.B = a->N; fp.s_q = 1; fp.topk = a->topk; fp.chunk = a->topk;
+    fp.B = a->N; fp.s_q = 1; fp.topk = a->topk;
+    fp.chunk = a->topk == 0 ? 0 : (a->topk + ns - 1) / ns;
     fp.causal = a->causal ? 2 : 0;
     fp.causal_offset = a->causal_offset;
     fp.reverse = 1;
     fp.scale_log2 = a->sm_scale * LOG2E;
-    return launch_fwd(fp, a->kv_format, a->N, 1, 1, (hipStream_t)stream);
+    return prefill_launch(fp, a->kv_format, ns, nullptr, ws, (hipStream_t)stream);
 }
 
-int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* a, void* stream) {
-    if (!a) return DSA_ERR_NULL_POINTER;
-    if (a->N < 0 || a->total_pages < 0 || a->total_tokens < 0 || a->max_rows < 0) return DSA_ERR_BAD_SHAPE;
-    // row ids carry their pool in bit 30 (dsa_rows.h): each pool stays below 2^30 rows
-    if (a->total_pages >= dsa_rows::MAX_POOL_ROWS || a->total_tokens >= dsa_rows::MAX_POOL_ROWS)
-        return DSA_ERR_BAD_SHAPE;
-    if (a->max_rows > MAX_LIST) return DSA_ERR_BAD_SHAPE;
-    if (!heads_ok(a->H, a->N)) return DSA_ERR_BAD_SHAPE;
-    if (a->D != DSA_MLA_D_V4) return DSA_ERR_UNSUPPORTED;
+int dsa_mla_prefill_v4_workspace_size(const dsa_mla_prefill_v4_args* a, size_t* bytes) {
+    if (!bytes) return DSA_ERR_NULL_POINTER;
+    int ns;
+    const int rc = validate_v4(a, &ns);
+    if (rc) return rc;
+    *bytes = prefill_ws_bytes(ns, a->N, a->H);
+    return DSA_OK;
+}
+
+int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* a, void* ws, size_t ws_bytes, void* stream) {
+    int ns;
+    const int rc = validate_v4(a, &ns);
+    if (rc) return rc;
+    const size_t need = prefill_ws_bytes(ns, a->N, a->H);
+    if (need && (!ws || ws_bytes < need || ((uintptr_t)ws & 15))) return DSA_ERR_WORKSPACE;
     if (a->N == 0) return DSA_OK;
-    if (!a->q || !a->out || !a->kv_indptr_prefix || !a->kv_indices_prefix || !a->kv_indptr_extend ||
-        !a->kv_indices_extend)
-        return DSA_ERR_NULL_POINTER;
-    if ((a->total_pages > 0 && !a->unified_kv) || (a->total_tokens > 0 && !a->kv)) return DSA_ERR_NULL_POINTER;
-    if (a->stride_qo_n < 0 || a->stride_qo_h < 0 || (a->stride_qo_n % 8) || (a->stride_qo_h % 8) ||
-        a->stride_kv_page < DSA_MLA_D_V4 || (a->stride_kv_page % 8))
-        return DSA_ERR_BAD_STRIDE;
-    if (((uintptr_t)a->q & 15) || ((uintptr_t)a->unified_kv & 15) || ((uintptr_t)a->kv & 15) ||
-        ((uintptr_t)a->out & 7))
-        return DSA_ERR_BAD_STRIDE;
     FwdParams fp{};
     fp.H = a->H;
     fp.hgroups = head_groups(a->H);
@@ -2432,38 +2543,30 @@ int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* a, void* stream) {
     fp.block_size = 1;
     fp.ind_pre = a->kv_indptr_prefix; fp.idx_pre = a->kv_indices_prefix;
     fp.ind_ext = a->kv_indptr_extend; fp.idx_ext = a->kv_indices_extend;
-    fp.attn_sink = a->attn_sink;
     fp.out = (__bf16*)a->out;
     fp.o_sb = a->stride_qo_n; fp.o_st = 0; fp.o_sh = a->stride_qo_h;
     fp.lse = a->lse;
     fp.B = a->N; fp.s_q = 1; fp.topk = a->max_rows; fp.chunk = a->max_rows;
     fp.scale_log2 = a->softmax_scale * LOG2E;
-    return launch_fwd(fp, DSA_KV_BF16_D512, a->N, 1, 1, (hipStream_t)stream);
+    return prefill_launch(fp, DSA_KV_BF16_D512, ns, a->attn_sink, ws, (hipStream_t)stream);
 }
-int dsa_mla_prefill_v4_fp8(const dsa_mla_prefill_v4_fp8_args* a, void* stream) {
-    if (!a) return DSA_ERR_NULL_POINTER;
-    if (a->N < 0 || a->total_pages < 0 || a->total_tokens < 0 || a->max_rows < 0) return DSA_ERR_BAD_SHAPE;
-    if (a->total_pages >= dsa_rows::MAX_POOL_ROWS || a->total_tokens >= dsa_rows::MAX_POOL_ROWS)
-        return DSA_ERR_BAD_SHAPE;
-    if (a->max_rows > MAX_LIST) return DSA_ERR_BAD_SHAPE;
-    if (!heads_ok(a->H, a->N)) return DSA_ERR_BAD_SHAPE;
+
+int dsa_mla_prefill_v4_fp8_workspace_size(const dsa_mla_prefill_v4_fp8_args* a, size_t* bytes) {
+    if (!bytes) return DSA_ERR_NULL_POINTER;
+    int ns;
+    const int rc = validate_v4fp8(a, &ns);
+    if (rc) return rc;
+    *bytes = prefill_ws_bytes(ns, a->N, a->H);
+    return DSA_OK;
+}
+
+int dsa_mla_prefill_v4_fp8(const dsa_mla_prefill_v4_fp8_args* a, void* ws, size_t ws_bytes, void* stream) {
+    int ns;
+    const int rc = validate_v4fp8(a, &ns);
+    if (rc) return rc;
+    const size_t need = prefill_ws_bytes(ns, a->N, a->H);
+    if (need && (!ws || ws_bytes < need || ((uintptr_t)ws & 15))) return DSA_ERR_WORKSPACE;
     if (a->N == 0) return DSA_OK;
-    if (!a->q_nope || !a->q_rope || !a->out || !a->kv_indptr_prefix || !a->kv_indices_prefix ||
-        !a->kv_indptr_extend || !a->kv_indices_extend)
-        return DSA_ERR_NULL_POINTER;
-    if ((a->total_pages > 0 && (!a->unified_kv_nope || !a->unified_kv_rope)) ||
-        (a->total_tokens > 0 && (!a->kv_nope || !a->kv_rope)))
-        return DSA_ERR_NULL_POINTER;
-    const int32_t b16[] = {a->stride_q_nope_n, a->stride_q_nope_h, a->stride_kv_nope_page};
-    for (int32_t v : b16) if (v < 0 || (v % 16)) return DSA_ERR_BAD_STRIDE;
-    if (a->stride_kv_nope_page < DSA_MLA_V4_NOPE_BYTES) return DSA_ERR_BAD_STRIDE;
-    const int32_t e8[] = {a->stride_q_rope_n, a->stride_q_rope_h, a->stride_kv_rope_page};
-    for (int32_t v : e8) if (v < 0 || (v % 8)) return DSA_ERR_BAD_STRIDE;
-    if (a->stride_o_n < 0 || a->stride_o_h < 0 || (a->stride_o_n % 4) || (a->stride_o_h % 4))
-        return DSA_ERR_BAD_STRIDE;
-    const void* ptrs[] = {a->q_nope, a->q_rope, a->unified_kv_nope, a->unified_kv_rope, a->kv_nope, a->kv_rope};
-    for (const void* q : ptrs) if ((uintptr_t)q & 15) return DSA_ERR_BAD_STRIDE;
-    if ((uintptr_t)a->out & 7) return DSA_ERR_BAD_STRIDE;
     FwdParams fp{};
     fp.H = a->H;
     fp.hgroups = head_groups(a->H);
@@ -2485,13 +2588,12 @@ int dsa_mla_prefill_v4_fp8(const dsa_mla_prefill_v4_fp8_args* a, void* stream) {
     fp.block_size = 1;
     fp.ind_pre = a->kv_indptr_prefix; fp.idx_pre = a->kv_indices_prefix;
     fp.ind_ext = a->kv_indptr_extend; fp.idx_ext = a->kv_indices_extend;
-    fp.attn_sink = a->attn_sink;
     fp.out = (__bf16*)a->out;
     fp.o_sb = a->stride_o_n; fp.o_st = 0; fp.o_sh = a->stride_o_h;
     fp.lse = a->lse;
     fp.B = a->N; fp.s_q = 1; fp.topk = a->max_rows; fp.chunk = a->max_rows;
     fp.scale_log2 = a->softmax_scale * LOG2E;
-    return launch_fwd(fp, DSA_KV_MXFP8_V4, a->N, 1, 1, (hipStream_t)stream);
+    return prefill_launch(fp, DSA_KV_MXFP8_V4, ns, a->attn_sink, ws, (hipStream_t)stream);
 }
 int dsa_kv_quantize_fp8(const void* src, int64_t src_stride, int64_t n_rows, void* dst, int64_t dst_total,
                         const int64_t* dst_rows, void* stream) {

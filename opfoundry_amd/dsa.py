@@ -57,6 +57,16 @@ def _need(t: torch.Tensor, dtype, name: str):
         raise ValueError(f"{name} must be a device tensor")
 
 
+def _run_with_workspace(size_fn, run_fn, args, workspace, device, stream, where: str):
+    """Size the call's workspace (size_fn), allocate one if the caller's is missing or too small,
+    and launch (run_fn(args, ws_ptr, ws_bytes, stream))."""
+    n = ctypes.c_size_t(0)
+    check(size_fn(ctypes.byref(args), ctypes.byref(n)), where + "_workspace_size")
+    if n.value and (workspace is None or workspace.numel() * workspace.element_size() < n.value):
+        workspace = torch.empty(n.value, dtype=torch.uint8, device=device)
+    check(run_fn(ctypes.byref(args), _ptr(workspace) if n.value else None, n.value, _stream(stream)), where)
+
+
 def make_decode_args(q, kv_cache, indices, sm_scale, out, lse, *, seq_lens, block_table=None,
                      block_size=None, causal=False, num_splits=0, kv_batch_stride=0):
     B, s_q, H, D = q.shape
@@ -317,7 +327,7 @@ def mla_combine(partial_o: torch.Tensor, partial_lse: torch.Tensor,
     return out, lse
 
 
-def make_prefill_args(q, kv, indices, sm_scale, out, lse, *, causal=False, causal_offset=0):
+def make_prefill_args(q, kv, indices, sm_scale, out, lse, *, causal=False, causal_offset=0, num_splits=0):
     N, H, D = q.shape
     if D != abi.D_QK or q.stride(2) != 1:
         raise ValueError("q must be [N, H, 576] with a dense last dim")
@@ -340,6 +350,7 @@ def make_prefill_args(q, kv, indices, sm_scale, out, lse, *, causal=False, causa
     a.causal = 1 if causal else 0
     a.causal_offset = int(causal_offset)
     a.sm_scale = float(sm_scale)
+    a.num_splits = int(num_splits)
     return a
 
 
@@ -352,10 +363,12 @@ def prefill_workspace_size(args: PrefillArgs) -> int:
 
 def mla_prefill(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor, sm_scale: float,
                 out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None, *,
-                causal: bool = False, causal_offset: int = 0,
+                causal: bool = False, causal_offset: int = 0, num_splits: int = 0,
                 workspace: Optional[torch.Tensor] = None,
                 stream=None) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Sparse MLA prefill: per-query top-k over one KV pool; returns (out bf16, lse fp32)."""
+    """Sparse MLA prefill: per-query top-k over one KV pool; returns (out bf16, lse fp32).
+    num_splits: split-K over each query's list (0 = automatic, more than one only for few
+    queries)."""
     _need(q, torch.bfloat16, "q")
     _need(indices, torch.int32, "indices")
     N, H, _ = q.shape
@@ -364,7 +377,7 @@ def mla_prefill(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor, sm_sca
     if lse is None:
         lse = torch.empty((N, H), dtype=torch.float32, device=q.device)
     a = make_prefill_args(q, kv, indices, sm_scale, out, lse, causal=causal,
-                          causal_offset=causal_offset)
+                          causal_offset=causal_offset, num_splits=num_splits)
     nbytes = prefill_workspace_size(a)
     if nbytes and (workspace is None or workspace.numel() * workspace.element_size() < nbytes):
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
@@ -378,10 +391,14 @@ def mla_prefill_v4(q: torch.Tensor, unified_kv: torch.Tensor, kv: torch.Tensor,
                    kv_indices_prefix: torch.Tensor, kv_indptr_extend: torch.Tensor,
                    kv_indices_extend: torch.Tensor, softmax_scale: float,
                    out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None, *,
-                   max_rows: Optional[int] = None, stream=None) -> Tuple[torch.Tensor, torch.Tensor]:
+                   max_rows: Optional[int] = None, num_splits: int = 0,
+                   workspace: Optional[torch.Tensor] = None,
+                   stream=None) -> Tuple[torch.Tensor, torch.Tensor]:
     """DeepSeek-V4 sparse prefill (opus_mla_v4_prefill_kargs form): q [N, H, 512] bf16, prefix
     rows from unified_kv [total_pages, 512], extend rows from kv [total_tokens, 512], per-head
-    attn_sink fp32 [H] in the softmax denominator (or None); returns (out [N, H, 512], lse [N, H])."""
+    attn_sink fp32 [H] in the softmax denominator (or None); returns (out [N, H, 512], lse [N, H]).
+    num_splits: split-K over each query's list (0 = automatic, more than one only for few
+    queries); the split partials live in `workspace` (allocated here when missing)."""
     _need(q, torch.bfloat16, "q")
     for t, n in ((unified_kv, "unified_kv"), (kv, "kv")):
         _need(t, torch.bfloat16, n)
@@ -417,7 +434,10 @@ def mla_prefill_v4(q: torch.Tensor, unified_kv: torch.Tensor, kv: torch.Tensor,
         raise ValueError("unified_kv and kv must share the row stride (stride_kv_page)")
     a.max_rows = int(max_rows)
     a.softmax_scale = float(softmax_scale)
-    check(load_library().dsa_mla_prefill_v4(ctypes.byref(a), _stream(stream)), "dsa_mla_prefill_v4")
+    a.num_splits = int(num_splits)
+    lib = load_library()
+    _run_with_workspace(lib.dsa_mla_prefill_v4_workspace_size, lib.dsa_mla_prefill_v4, a, workspace,
+                        q.device, stream, "dsa_mla_prefill_v4")
     return out, lse
 
 
@@ -478,7 +498,9 @@ def mla_prefill_v4_fp8(q_nope: torch.Tensor, q_rope: torch.Tensor, unified_kv_no
                        kv_indices_prefix: torch.Tensor, kv_indptr_extend: torch.Tensor,
                        kv_indices_extend: torch.Tensor, softmax_scale: float,
                        out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None, *,
-                       max_rows: Optional[int] = None, stream=None) -> Tuple[torch.Tensor, torch.Tensor]:
+                       max_rows: Optional[int] = None, num_splits: int = 0,
+                       workspace: Optional[torch.Tensor] = None,
+                       stream=None) -> Tuple[torch.Tensor, torch.Tensor]:
     """DeepSeek-V4 sparse prefill on fp8 rows (opus_mla_v4_prefill_fp8_kargs form): every row and
     Q head is a 512-byte NoPE stream row (448 e4m3 codes, 14 E8M0 scales, pad; uint8) plus 64 bf16
     RoPE values; q_* [N, H, 512 | 64], pools [rows, 512 | 64].  Returns (out bf16 [N, H, 512],
@@ -525,7 +547,10 @@ def mla_prefill_v4_fp8(q_nope: torch.Tensor, q_rope: torch.Tensor, unified_kv_no
     a.stride_kv_nope_page, a.stride_kv_rope_page = unified_kv_nope.stride(0), unified_kv_rope.stride(0)
     a.max_rows = int(max_rows)
     a.softmax_scale = float(softmax_scale)
-    check(load_library().dsa_mla_prefill_v4_fp8(ctypes.byref(a), _stream(stream)), "dsa_mla_prefill_v4_fp8")
+    a.num_splits = int(num_splits)
+    lib = load_library()
+    _run_with_workspace(lib.dsa_mla_prefill_v4_fp8_workspace_size, lib.dsa_mla_prefill_v4_fp8, a, workspace,
+                        q_nope.device, stream, "dsa_mla_prefill_v4_fp8")
     return out, lse
 
 

@@ -183,6 +183,57 @@ static void load_row(const uint8_t* cache, int fmt, int64_t row_bytes, int64_t r
 /* ------------------------------------------------------ attention core */
 
 /*
+ * scores[p] = (q . row_p) * scale over n rows of width D (row stride D), each
+ * dot product summed in dim order, one fp32 multiply then one add per dim, as
+ * host.cc:437-438 and mla_v4_host.cc:463-466 write it.  Four rows at a time:
+ * their four sums are independent, so they overlap, and every row's sum sees
+ * exactly the operations of the one-row loop.
+ */
+static void dot_rows(const float* q, const float* kv, int n, int D, float scale, float* scores) {
+    int p = 0;
+    for (; p + 4 <= n; p += 4) {
+        const float* k0 = kv + (size_t)p * D;
+        const float* k1 = k0 + D;
+        const float* k2 = k1 + D;
+        const float* k3 = k2 + D;
+        float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
+        for (int d = 0; d < D; ++d) {
+            const float x = q[d];
+            d0 += x * k0[d];
+            d1 += x * k1[d];
+            d2 += x * k2[d];
+            d3 += x * k3[d];
+        }
+        scores[p] = d0 * scale;
+        scores[p + 1] = d1 * scale;
+        scores[p + 2] = d2 * scale;
+        scores[p + 3] = d3 * scale;
+    }
+    for (; p < n; ++p) {
+        const float* k = kv + (size_t)p * D;
+        float dot = 0.0f;
+        for (int d = 0; d < D; ++d) dot += q[d] * k[d];
+        scores[p] = dot * scale;
+    }
+}
+
+/*
+ * acc[d] = sum_p w[p] * row_p[d] for d < D (rows `stride` floats apart), each
+ * sum taken over the rows in list order from 0.0f, as host.cc:452-456 and
+ * mla_v4_host.cc:473-477 write it.  Rows outer, dims inner: the rows are read
+ * once, in order, and every output sees exactly the operations of the
+ * dims-outer loop.
+ */
+static void weighted_rows(const float* w, const float* kv, int n, int stride, int D, float* acc) {
+    for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+    for (int p = 0; p < n; ++p) {
+        const float s = w[p];
+        const float* r = kv + (size_t)p * stride;
+        for (int d = 0; d < D; ++d) acc[d] += s * r[d];
+    }
+}
+
+/*
  * One (token, head): host.cc:431-457 with sm_scale as a parameter.
  * Writes either the final row (o_bf16 != NULL: bf16 O and LSE, O = 0 and
  * LSE = +inf when n == 0, host.cc:486-489) or a split partial (o_f32: fp32 O
@@ -199,23 +250,18 @@ static void attention_core(const float* q, const float* kv, int n, float sm_scal
         if (lse) *lse = o_bf16 ? INFINITY : -FLT_MAX;
         return;
     }
-    for (int p = 0; p < n; ++p) {
-        const float* k = kv + (size_t)p * D_QK;
-        float dot = 0.0f;
-        for (int d = 0; d < D_QK; ++d) dot += q[d] * k[d];
-        scores[p] = dot * sm_scale;
-    }
+    dot_rows(q, kv, n, D_QK, sm_scale, scores);
     float mx = scores[0];
     for (int p = 1; p < n; ++p) if (scores[p] > mx) mx = scores[p];
     float sum = 0.0f;
     for (int p = 0; p < n; ++p) { scores[p] = expf(scores[p] - mx); sum += scores[p]; }
     if (lse) *lse = logf(sum) + mx;
     for (int p = 0; p < n; ++p) scores[p] = oracle_bf16_to_f32(oracle_f32_to_bf16(scores[p] / sum));
+    float acc[D_VO];
+    weighted_rows(scores, kv, n, D_QK, D_VO, acc);
     for (int d = 0; d < D_VO; ++d) {
-        float acc = 0.0f;
-        for (int p = 0; p < n; ++p) acc += scores[p] * kv[(size_t)p * D_QK + d];
-        if (o_bf16) o_bf16[d] = oracle_f32_to_bf16(acc);
-        if (o_f32) o_f32[d] = acc;
+        if (o_bf16) o_bf16[d] = oracle_f32_to_bf16(acc[d]);
+        if (o_f32) o_f32[d] = acc[d];
     }
 }
 
@@ -425,12 +471,7 @@ static void attention_core_v4(const float* q, const float* kv, int n, float scal
         if (lse) *lse = INFINITY;
         return;
     }
-    for (int p = 0; p < n; ++p) {
-        const float* k = kv + (size_t)p * D;
-        float dot = 0.0f;
-        for (int d = 0; d < D; ++d) dot += q[d] * k[d];
-        scores[p] = dot * scale;
-    }
+    dot_rows(q, kv, n, D, scale, scores);
     float mx = sink;
     for (int p = 0; p < n; ++p) if (scores[p] > mx) mx = scores[p];
     float sum = 0.0f;
@@ -438,11 +479,9 @@ static void attention_core_v4(const float* q, const float* kv, int n, float scal
     sum += expf(sink - mx);
     if (lse) *lse = logf(sum) + mx;
     for (int p = 0; p < n; ++p) scores[p] = oracle_bf16_to_f32(oracle_f32_to_bf16(scores[p] / sum));
-    for (int d = 0; d < D; ++d) {
-        float acc = 0.0f;
-        for (int p = 0; p < n; ++p) acc += scores[p] * kv[(size_t)p * D + d];
-        o_bf16[d] = oracle_f32_to_bf16(acc);
-    }
+    float acc[DSA_MLA_D_V4];
+    weighted_rows(scores, kv, n, D, D, acc);
+    for (int d = 0; d < D; ++d) o_bf16[d] = oracle_f32_to_bf16(acc[d]);
 }
 
 typedef struct {

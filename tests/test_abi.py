@@ -217,7 +217,7 @@ def test_row_strides_accepted(lib):
         assert _ws(lib, _decode_args(kv_format=fmt, kv_stride_row=st))[0] == 0
         assert _csr_ws(lib, _csr_args(kv_format=fmt, stride_kv_page=st))[0] == 0
     ok = _v4_args(total_pages=(1 << 30) - 1, total_tokens=(1 << 30) - 1, N=0)
-    assert lib.dsa_mla_prefill_v4(ctypes.byref(ok), None) == 0
+    assert lib.dsa_mla_prefill_v4(ctypes.byref(ok), None, 0, None) == 0
 
 
 def test_csr_split_plan():
@@ -352,11 +352,11 @@ def _v4_args(**kw):
     (dict(total_pages=1 << 30), -2), (dict(total_tokens=1 << 30), -2), (dict(total_pages=2 ** 31 - 1), -2),
 ])
 def test_prefill_v4_rejects_bad_arguments(lib, kw, code):
-    assert lib.dsa_mla_prefill_v4(ctypes.byref(_v4_args(**kw)), None) == code
+    assert lib.dsa_mla_prefill_v4(ctypes.byref(_v4_args(**kw)), None, 0, None) == code
 
 
 def test_prefill_v4_empty_is_a_no_op(lib):
-    assert lib.dsa_mla_prefill_v4(ctypes.byref(_v4_args(N=0)), None) == 0
+    assert lib.dsa_mla_prefill_v4(ctypes.byref(_v4_args(N=0)), None, 0, None) == 0
 
 
 def _prefill_args(**kw):
@@ -447,14 +447,14 @@ def _v4fp8_args(**kw):
     (dict(total_pages=1 << 30), -2), (dict(total_tokens=1 << 30), -2),
 ])
 def test_prefill_v4_fp8_rejects_bad_arguments(lib, kw, code):
-    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(_v4fp8_args(**kw)), None) == code
+    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(_v4fp8_args(**kw)), None, 0, None) == code
 
 
 def test_prefill_v4_fp8_empty_is_a_no_op(lib):
-    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(_v4fp8_args(N=0)), None) == 0
+    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(_v4fp8_args(N=0)), None, 0, None) == 0
     # empty pools need no pool pointers
     a = _v4fp8_args(N=0, total_pages=0, unified_kv_nope=None, unified_kv_rope=None)
-    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(a), None) == 0
+    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(a), None, 0, None) == 0
 
 
 def test_long_lists_accepted_unsplit(lib):
@@ -469,8 +469,8 @@ def test_long_lists_accepted_unsplit(lib):
     n = ctypes.c_size_t(1)
     assert lib.dsa_mla_prefill_workspace_size(ctypes.byref(_prefill_args(topk=4096)), ctypes.byref(n)) == 0
     assert n.value == 0
-    assert lib.dsa_mla_prefill_v4(ctypes.byref(_v4_args(max_rows=1 << 20, N=0)), None) == 0
-    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(_v4fp8_args(max_rows=1 << 20, N=0)), None) == 0
+    assert lib.dsa_mla_prefill_v4(ctypes.byref(_v4_args(max_rows=1 << 20, N=0)), None, 0, None) == 0
+    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(_v4fp8_args(max_rows=1 << 20, N=0)), None, 0, None) == 0
 
 
 def test_max_list_bound(lib):
@@ -493,8 +493,8 @@ def test_any_head_count_accepted(lib, H):
     assert _csr_ws(lib, _csr_args(H=H))[0] == 0
     n = ctypes.c_size_t(1)
     assert lib.dsa_mla_prefill_workspace_size(ctypes.byref(_prefill_args(H=H)), ctypes.byref(n)) == 0
-    assert lib.dsa_mla_prefill_v4(ctypes.byref(_v4_args(H=H, N=0)), None) == 0
-    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(_v4fp8_args(H=H, N=0)), None) == 0
+    assert lib.dsa_mla_prefill_v4(ctypes.byref(_v4_args(H=H, N=0)), None, 0, None) == 0
+    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(_v4fp8_args(H=H, N=0)), None, 0, None) == 0
 
 
 def test_head_groups_bound_the_grid(lib):
@@ -551,3 +551,41 @@ def test_indexer_empty_is_a_no_op(lib):
         assert lib.dsa_indexer_scores(ctypes.byref(_ix_args(**kw)), None) == 0
     # no k rows at all: accepted (every position scores -inf), k_cache may be NULL
     assert lib.dsa_indexer_scores(ctypes.byref(_ix_args(k_total_rows=0, k_cache=None, B=0)), None) == 0
+
+
+def _prefill_ws(lib, fn, a):
+    n = ctypes.c_size_t(0)
+    rc = fn(ctypes.byref(a), ctypes.byref(n))
+    return rc, n.value
+
+
+def test_prefill_split_workspace(lib):
+    """Split-K prefill: automatic splits only when fewer than 256 workgroups would run (at
+    least 256 list entries per split), the workspace holding num_splits x N x H x 513 floats;
+    explicit counts 1..64; a missing or short workspace is rejected before any launch."""
+    per = 128 * 513 * 4
+    # C5-sized: 8192 queries, unsplit, no workspace
+    assert _prefill_ws(lib, lib.dsa_mla_prefill_workspace_size, _prefill_args()) == (0, 0)
+    # 16 queries of a 65536-entry list: 16 splits
+    rc, n = _prefill_ws(lib, lib.dsa_mla_prefill_workspace_size, _prefill_args(N=16, topk=65536))
+    assert rc == 0 and n == 16 * 16 * per + 256
+    # short lists keep >= 256 entries per split
+    rc, n = _prefill_ws(lib, lib.dsa_mla_prefill_workspace_size, _prefill_args(N=16, topk=600))
+    assert rc == 0 and n == 2 * 16 * per + 256
+    rc, n = _prefill_ws(lib, lib.dsa_mla_prefill_workspace_size, _prefill_args(N=8192, num_splits=3))
+    assert rc == 0 and n == 3 * 8192 * per + 256
+    for bad in (-1, 65):
+        assert _prefill_ws(lib, lib.dsa_mla_prefill_workspace_size, _prefill_args(num_splits=bad))[0] == -6
+    # V4 bf16 / fp8: the harness's -n 16 -topk 0 over 65536 pages
+    rc, n = _prefill_ws(lib, lib.dsa_mla_prefill_v4_workspace_size, _v4_args(N=16, max_rows=65536 + 128))
+    assert rc == 0 and n == 16 * 16 * per + 256
+    rc, n = _prefill_ws(lib, lib.dsa_mla_prefill_v4_fp8_workspace_size, _v4fp8_args(N=16, max_rows=65536 + 128))
+    assert rc == 0 and n == 16 * 16 * per + 256
+    rc, n = _prefill_ws(lib, lib.dsa_mla_prefill_v4_workspace_size, _v4_args(N=4096))
+    assert rc == 0 and n == 0
+    assert _prefill_ws(lib, lib.dsa_mla_prefill_v4_workspace_size, _v4_args(num_splits=65))[0] == -6
+    assert _prefill_ws(lib, lib.dsa_mla_prefill_v4_fp8_workspace_size, _v4fp8_args(num_splits=-2))[0] == -6
+    # a split call without (or with too small) a workspace: DSA_ERR_WORKSPACE, nothing launched
+    assert lib.dsa_mla_prefill_v4(ctypes.byref(_v4_args(num_splits=4)), None, 0, None) == -5
+    assert lib.dsa_mla_prefill_v4_fp8(ctypes.byref(_v4fp8_args(num_splits=4)), 0x10000, 1024, None) == -5
+    assert lib.dsa_mla_prefill(ctypes.byref(_prefill_args(num_splits=2)), None, 0, None) == -5
