@@ -200,10 +200,47 @@ __host__ __device__ inline int plan_item_slot(int w) { return (w & (PLAN_LAST - 
 // max_kv_len it was built for
 constexpr int PLAN_HDR_B = 3, PLAN_HDR_SQ = 4, PLAN_HDR_MAXLEN = 5;
 
-// Physical cache row of logical position j of query (b, t); -1 if invalid.
-__device__ __forceinline__ int64_t resolve_row(const FwdParams& p, int b, int64_t jmax, int32_t j) {
-    return dsa_rows::topk_row(j, jmax, p.block_table ? p.block_table + (int64_t)b * p.bt_stride : nullptr,
-                              p.block_size, p.bs_shift, (int64_t)b * p.kv_batch_stride, p.kv_total_rows);
+// Inclusive prefix sum over the wave's lanes of v (0 <= v < 16): from the
+// ballots of v's four bits, each counted below the lane (v_mbcnt), with no
+// LDS round trip.
+__device__ __forceinline__ int wave_incl_sum16(int v) {
+    int excl = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint64_t m = __builtin_amdgcn_ballot_w64(((v >> k) & 1) != 0);
+        excl += (int)__builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u)) << k;
+    }
+    return excl + v;
+}
+
+// Physical cache rows of top-k entries jv of query b (-1 where skipped): the
+// block-table reads of all N entries are issued before any is waited for
+// (one memory round trip, not N).
+template <int N>
+__device__ __forceinline__ void topk_rows(const FwdParams& p, int b, int64_t jmax, const int32_t (&jv)[N],
+                                          int32_t (&rows)[N]) {
+    const int64_t flat = (int64_t)b * p.kv_batch_stride;
+    if (p.block_table) {
+        const int32_t* bt = p.block_table + (int64_t)b * p.bt_stride;
+        // the block-table entry of each entry's block, -1 for a skipped entry
+        // (a negative entry is skipped as well: its rows are below 0)
+        int32_t ent[N];
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+            const int32_t blk = dsa_rows::topk_block(jv[e], jmax, p.block_size, p.bs_shift);
+            ent[e] = blk >= 0 ? bt[blk] : -1;
+        }
+#pragma unroll
+        for (int e = 0; e < N; ++e)
+            rows[e] = ent[e] < 0 ? -1
+                                 : (int32_t)dsa_rows::topk_finish(jv[e], 0, ent[e], true, p.block_size, p.bs_shift,
+                                                                  flat, p.kv_total_rows);
+    } else {
+#pragma unroll
+        for (int e = 0; e < N; ++e)
+            rows[e] = (int32_t)dsa_rows::topk_finish(jv[e], dsa_rows::topk_block(jv[e], jmax, p.block_size, p.bs_shift),
+                                                     0, false, p.block_size, p.bs_shift, flat, p.kv_total_rows);
+    }
 }
 
 // One piece of the fp8 dequant in flight: codes + scale, or 16 RoPE bytes.
@@ -525,23 +562,21 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                 if (k >= kc1) jv[e] = -1;
                 else jv[e] = ext[e] ? p.idx_ext[v4_eb + (k - v4_np)] : idx[k];
             }
+            if (L::D512 && p.ind_pre) {
 #pragma unroll
-            for (int e = 0; e < PER_T; ++e) {
-                if (L::D512 && p.ind_pre)
+                for (int e = 0; e < PER_T; ++e)
                     rows_local[e] = ext[e] ? dsa_rows::v4_extend_row(jv[e], p.kv2_rows)
                                            : dsa_rows::v4_prefix_row(jv[e], p.kv_total_rows);
-                else
-                    rows_local[e] = p.kv_indptr ? dsa_rows::csr_row(jv[e], p.kv_total_rows)
-                                                : (int32_t)resolve_row(p, b, jmax, jv[e]);
-                cnt += rows_local[e] >= 0 ? 1 : 0;
-            }
-        }
-        int incl = cnt;
+            } else if (p.kv_indptr) {
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int v = __shfl_up(incl, off, 64);
-            if (lane >= off) incl += v;
+                for (int e = 0; e < PER_T; ++e) rows_local[e] = dsa_rows::csr_row(jv[e], p.kv_total_rows);
+            } else {
+                topk_rows(p, b, jmax, jv, rows_local);
+            }
+#pragma unroll
+            for (int e = 0; e < PER_T; ++e) cnt += rows_local[e] >= 0 ? 1 : 0;
         }
+        const int incl = wave_incl_sum16(cnt);
         // (the barrier also ends every wave's use of the previous chunk's
         // row list, tile buffers and P buffers)
         if (lane == 63) s_misc[wave] = incl;
@@ -1574,6 +1609,484 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Narrow forward kernel (bf16 576-value rows; top-k form, or CSR form with
+// uniform splits): one workgroup per (query token, group of 32 heads, split).
+// For few query tokens (low-batch decode) and small head counts: a 128-head
+// workgroup per token leaves most CUs idle, or computes padding heads, while
+// 32-head groups give 4x the workgroups, each with a quarter of the Q load, of
+// the MFMA work per tile and of the output.  Rules as in
+// dsa_mla_fwd_kernel<DSA_KV_BF16>; per tile of 32 rows:
+//   QK^T     wave w = 2 hb + rb computes S^T[rows 16 rb.. x heads 16 hb..]
+//            with 16x16x32 MFMAs, its 16 heads' Q in registers (each K row is
+//            read by two waves, no partial scores cross the waves)
+//   softmax  fixed reference (the first tile's maximum per head, taken over
+//            both row halves through LDS) with one restart; 4 exponentials
+//            per lane; P (bf16) goes to LDS in the PV operand layout
+//   PV       split by output dims: wave w accumulates O^T[dims 128w.. x 32 heads]
+// Two workgroup barriers per tile (tile landed; P written).
+// grid = (B * ceil(H / 32), s_q, num_splits), block = 256.
+// ---------------------------------------------------------------------------
+constexpr int NARROW_HEADS = 32;
+constexpr int NKS = D_QK / 32;                // 32-deep k-steps of QK^T (16 NoPE, 2 RoPE)
+constexpr int P_BYTES = 2 * 2 * 32 * 16;      // P of a tile: [u][hi][head] x 8 bf16
+
+__device__ __forceinline__ f32x4 mfma16_bf16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+// A global-memory pointer from its address (a generic pointer of unknown
+// origin would be accessed with flat loads).
+template <class T>
+__device__ __forceinline__ T* gptr(uintptr_t u) {
+    return (T*)(__attribute__((address_space(1))) T*)u;
+}
+
+// A wave-uniform int32 read through the scalar cache (the constant address
+// space: an s_load, counted apart from the vector loads, so that waiting for it
+// does not wait for vector loads issued earlier).  For data no kernel of the
+// call writes.
+__device__ __forceinline__ int32_t sload(const int32_t* ptr) {
+    return *(const __attribute__((address_space(4))) int32_t*)(uintptr_t)ptr;
+}
+
+__global__ void __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(1, 1)))
+dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
+    __shared__ __attribute__((aligned(1024))) unsigned char s_tiles[3 * TILE_BYTES];
+    __shared__ __attribute__((aligned(16))) unsigned char s_p[P_BYTES];
+    __shared__ int32_t s_rows_arr[MAX_CHUNK];
+    // per-head values of the two row halves: [0] first-tile maxima, [1] one-tile
+    // sums, [2] pass maxima, [3] final sums; then the references
+    __shared__ float s_red_arr[4 * 2 * NARROW_HEADS + NARROW_HEADS];
+    __shared__ int s_misc_arr[NWAVE + 1];    // [0..3] wave counts, [4] restart flag
+    const lds_ptr TB = (lds_ptr)s_tiles;
+    const lds_ptr PX = (lds_ptr)s_p;
+    LDS_AS int32_t* const s_rows = (LDS_AS int32_t*)s_rows_arr;
+    LDS_AS float* const s_red = (LDS_AS float*)s_red_arr;
+    LDS_AS int* const s_misc = (LDS_AS int*)s_misc_arr;
+    // The arguments the prologue reads, copied into registers in one batch
+    // (opaque copies, which the compiler cannot reload where they are used):
+    // left to the compiler, the scalar loads of the argument block form a
+    // chain across the branches below, one memory round trip each.
+    FwdParams p = p_arg;
+    unsigned grid_x = gridDim.x, grid_z = gridDim.z;
+    uintptr_t a_q = (uintptr_t)p.q, a_bt = (uintptr_t)p.block_table, a_sl = (uintptr_t)p.seq_lens,
+              a_ix = (uintptr_t)p.indices, a_ip = (uintptr_t)p.kv_indptr, a_ki = (uintptr_t)p.kv_indices;
+    uintptr_t a_o = (uintptr_t)p.out, a_lse = (uintptr_t)p.lse, a_po = (uintptr_t)p.part_o, a_pl = (uintptr_t)p.part_lse;
+    asm volatile(""
+                 : "+s"(grid_x), "+s"(grid_z), "+s"(a_q), "+s"(a_bt), "+s"(a_sl), "+s"(a_ix), "+s"(a_ip), "+s"(a_ki),
+                   "+s"(p.q_sb), "+s"(p.q_st), "+s"(p.q_sh), "+s"(p.kv_total_rows), "+s"(p.kv_batch_stride),
+                   "+s"(p.bt_stride), "+s"(p.block_size), "+s"(p.bs_shift), "+s"(p.seq_len_default), "+s"(p.idx_sb),
+                   "+s"(p.idx_st), "+s"(p.s_q), "+s"(p.topk), "+s"(p.chunk), "+s"(p.H), "+s"(p.hgroups),
+                   "+s"(p.causal), "+s"(p.causal_offset), "+s"(p.reverse), "+s"(a_o), "+s"(p.o_sb), "+s"(p.o_st),
+                   "+s"(p.o_sh), "+s"(a_lse), "+s"(a_po), "+s"(a_pl));
+    p.out = gptr<__bf16>(a_o);
+    p.lse = gptr<float>(a_lse);
+    p.part_o = gptr<float>(a_po);
+    p.part_lse = gptr<float>(a_pl);
+    p.q = gptr<const __bf16>(a_q);
+    p.block_table = gptr<const int32_t>(a_bt);
+    p.seq_lens = gptr<const int32_t>(a_sl);
+    p.indices = gptr<const int32_t>(a_ix);
+    p.kv_indptr = gptr<const int32_t>(a_ip);
+    p.kv_indices = gptr<const int32_t>(a_ki);
+
+    // blockIdx.x = query token * hgroups + head group
+    const int gx = (int)blockIdx.x / p.hgroups;
+    const int hbase = NARROW_HEADS * ((int)blockIdx.x % p.hgroups);
+    const int b = p.reverse ? (int)(grid_x / p.hgroups) - 1 - gx : gx, t = blockIdx.y;
+    const int split = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rb = wave & 1, hb = wave >> 1;      // QK^T: row half, head half
+    const int c16 = lane & 15, g4 = lane >> 4;    // 16x16 operand lanes
+    const int hi = lane >> 5, r32 = lane & 31;    // PV and epilogue lanes: head r32
+    const int hq = 16 * hb + c16;                 // this lane's head in QK^T and the softmax
+    // heads past H are computed on a copy of head H-1 and never stored
+    const int head_g = hbase + r32;
+    if (tid == 0) s_misc[NWAVE] = 0;
+
+    // ---- this split's entries, by the rules of dsa_mla_fwd_kernel.  Top-k
+    // form: logical positions through the block table, bounded by seq_len and
+    // the causal rule.  CSR form (uniform splits): physical rows
+    // kv_indices[kv_indptr[b] + k], k below the count-based MTP bound ----
+    const int k0 = split * p.chunk;
+    int k1;
+    const int32_t* idx;
+    bool truncated = false;
+    if (p.kv_indptr) {
+        const int64_t kb = sload(p.kv_indptr + b);
+        const int64_t count = (int64_t)sload(p.kv_indptr + b + 1) - kb - (p.s_q - 1 - t);
+        k1 = (int)min((int64_t)k0 + p.chunk, count);
+        // a list longer than the splits cover (max_kv_len) is cut: NaN
+        truncated = count > (int64_t)grid_z * p.chunk;
+        idx = p.kv_indices + kb;
+    } else {
+        k1 = (int)min((int64_t)k0 + p.chunk, (int64_t)p.topk);
+        idx = p.indices + (int64_t)b * p.idx_sb + (int64_t)t * p.idx_st;
+    }
+    const int nchunks = k1 > k0 ? (k1 - k0 + MAX_CHUNK - 1) / MAX_CHUNK : 1;
+    constexpr int PER_T = MAX_CHUNK / NTHR;       // entries per thread and chunk
+    // the entries of chunk c (-1 past the split's end)
+    auto load_entries = [&](int c, int32_t (&jv)[PER_T]) {
+        const int kc0 = k0 + c * MAX_CHUNK;
+        const int kc1 = min(kc0 + MAX_CHUNK, k1);
+#pragma unroll
+        for (int e = 0; e < PER_T; ++e) {
+            const int k = kc0 + tid * PER_T + e;
+            jv[e] = k < kc1 ? idx[k] : -1;
+        }
+    };
+    // Chunk 0's entries are loaded before Q: vmcnt counts in order, so the wait
+    // for them does not wait for the Q loads as well.
+    int32_t jv0[PER_T];
+    load_entries(0, jv0);
+
+    // ---- Q fragments (B operand of S^T = K Q^T): head hq, dims 32 ks + 8 g4 .. +7 ----
+    u32x4 qf[NKS];
+    {
+        const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st +
+                           (int64_t)min(hbase + hq, p.H - 1) * p.q_sh + 8 * g4;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
+    }
+    // top-k form: the bound on positions, from seq_len and the causal rule
+    // (a scalar load, in flight with the entries and Q)
+    int64_t jmax = 0;
+    if (!p.kv_indptr) {
+        const int64_t Lq = p.seq_lens ? (int64_t)sload(p.seq_lens + b) : p.seq_len_default;
+        jmax = Lq;
+        if (p.causal == 1) jmax = min(Lq, Lq - p.s_q + t + 1);
+        else if (p.causal == 2) jmax = min(Lq, (int64_t)b + p.causal_offset + 1);
+    }
+    // chunk 0's entries have landed (the NKS Q loads per lane, issued after
+    // them, may still be in flight)
+    wait_vm<NKS>();
+
+    // entries of chunk c -> the compacted row list, the last tile padded with
+    // copies of the first valid row (ends with a barrier)
+    int n_valid = 0, ntiles = 0;
+    bool any_rows = false;
+    auto resolve_chunk = [&](int c, bool preloaded) {
+        int32_t rows_local[PER_T];
+        int cnt = 0;
+        {
+            int32_t jv[PER_T];
+            if (preloaded) {
+#pragma unroll
+                for (int e = 0; e < PER_T; ++e) jv[e] = jv0[e];
+            } else {
+                load_entries(c, jv);
+            }
+            if (p.kv_indptr) {
+#pragma unroll
+                for (int e = 0; e < PER_T; ++e) rows_local[e] = dsa_rows::csr_row(jv[e], p.kv_total_rows);
+            } else {
+                topk_rows(p, b, jmax, jv, rows_local);
+            }
+#pragma unroll
+            for (int e = 0; e < PER_T; ++e) cnt += rows_local[e] >= 0 ? 1 : 0;
+        }
+        const int incl = wave_incl_sum16(cnt);
+        // (the barrier also ends every wave's use of the previous chunk's row
+        // list, tile buffers and P)
+        if (lane == 63) s_misc[wave] = incl;
+        __syncthreads();
+        int wbase = 0, nv = 0;
+#pragma unroll
+        for (int w = 0; w < NWAVE; ++w) {
+            const int s = s_misc[w];
+            wbase += w < wave ? s : 0;
+            nv += s;
+        }
+        {
+            int pos = wbase + incl - cnt;
+#pragma unroll
+            for (int e = 0; e < PER_T; ++e)
+                if (rows_local[e] >= 0) s_rows[pos++] = rows_local[e];
+        }
+        // (wave-uniform: every wave summed the same counts)
+        n_valid = __builtin_amdgcn_readfirstlane(nv);
+        ntiles = (n_valid + TILE - 1) / TILE;
+        any_rows = any_rows || nv > 0;
+        __syncthreads();
+        if (tid < TILE && nv > 0 && nv + tid < ntiles * TILE) s_rows[nv + tid] = s_rows[0];
+        __syncthreads();
+    };
+
+    // ---- gather: wave w loads NoPE rows 8w..8w+7 (one 1 KB LDS-DMA load per
+    // row) and the RoPE blocks of those rows (one load); tile layout and
+    // swizzles as in dsa_mla_fwd_kernel ----
+    struct GatherRows {
+        int32_t r[TILE / NWAVE];   // this wave's rows (uniform)
+        int32_t rope;              // row of this lane's RoPE chunk
+    };
+    auto slot = [&](int s) -> lds_ptr { return TB + s * TILE_BYTES; };
+    auto load_rows = [&](int ti) -> GatherRows {
+        const LDS_AS int32_t* rows = s_rows + ti * TILE;
+        GatherRows g;
+        const u32x4 ra = lds_ld<u32x4>((lds_cptr)(rows + 8 * wave));
+        const u32x4 rv = lds_ld<u32x4>((lds_cptr)(rows + 8 * wave + 4));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            g.r[i] = __builtin_amdgcn_readfirstlane((int)ra[i]);
+            g.r[4 + i] = __builtin_amdgcn_readfirstlane((int)rv[i]);
+        }
+        g.rope = rows[8 * wave + (opaque(lane) >> 3)];
+        return g;
+    };
+    auto issue_rows = [&](const GatherRows& g, lds_ptr tb) {
+        const int ln = opaque(lane);
+#pragma unroll
+        for (int i = 0; i < TILE / NWAVE; ++i) {
+            const int r = 8 * wave + i;
+            lds_dma16_s(p.kv + (int64_t)__builtin_amdgcn_readfirstlane(g.r[i]) * p.row_bytes,
+                        16u * (unsigned)(ln ^ nope_sw(r)), tb + r * NOPE_STRIDE);
+        }
+        const int r = 8 * wave + (ln >> 3);
+        lds_dma16(p.kv + (int64_t)g.rope * p.row_bytes + 2 * D_NOPE + 16 * ((ln & 7) ^ rope_sw(r)),
+                  tb + ROPE_OFF + 8 * wave * 128);
+    };
+    constexpr int LPW = TILE / NWAVE + 1;     // loads per wave per tile
+
+    // ---- S^T[16 rows x 16 heads] = K Q^T (A operand: row 16 rb + c16, dims
+    // 32 ks + 8 g4 .. +7, i.e. chunk 4 ks + g4 at its swizzled position) ----
+    auto qk16 = [&](lds_cptr kt) -> f32x4 {
+        const int ln = opaque(lane);
+        const int row = 16 * rb + (ln & 15), lg = ln >> 4;
+        const lds_cptr kn = kt + row * NOPE_STRIDE + 16 * (lg ^ nope_sw(row));
+        const lds_cptr kr = kt + ROPE_OFF + 128 * row;
+        const int rsw = rope_sw(row);
+        auto k_addr = [&](int ks) -> lds_cptr {
+            return ks < KS_NOPE / 2 ? kn + 64 * ks : kr + 16 * ((4 * (ks - KS_NOPE / 2) + lg) ^ rsw);
+        };
+        constexpr int KPF = 6;
+        u32x4 kb[KPF];
+#pragma unroll
+        for (int i = 0; i < KPF; ++i) kb[i] = lds_ld<u32x4>(k_addr(i));
+        // two accumulator chains (a single 16x16x32 chain is latency-bound)
+        f32x4 acc[2] = {};
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            __builtin_amdgcn_sched_barrier(0);
+            acc[ks & 1] = mfma16_bf16(kb[ks % KPF], qf[ks], acc[ks & 1]);
+            if (ks + KPF < NKS) kb[ks % KPF] = lds_ld<u32x4>(k_addr(ks + KPF));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        return acc[0] + acc[1];
+    };
+
+    // softmax state of head hq over this wave's rows: lane (g4, c16), value i
+    // of the 16x16 tile is row 16 rb + 4 g4 + i of the tile
+    const float c_s = p.scale_log2;
+    float m_ref = 0.0f, l_lane = 0.0f, s_max = -INFINITY;
+    bool first_tile = true;
+    // per head over the wave's 16 rows (the 4 lanes g4 of head c16)
+    auto red4_max = [&](float v) {
+        v = fmaxf(v, __shfl_xor(v, 16, 64));
+        return fmaxf(v, __shfl_xor(v, 32, 64));
+    };
+    auto red4_sum = [&](float v) {
+        v += __shfl_xor(v, 16, 64);
+        return v + __shfl_xor(v, 32, 64);
+    };
+    // per-head value of both row halves through LDS slot k (a barrier between)
+    auto put_half = [&](int k, float v) {
+        if (g4 == 0) s_red[(2 * k + rb) * NARROW_HEADS + hq] = v;
+    };
+    auto get_max = [&](int k) { return fmaxf(s_red[2 * k * NARROW_HEADS + hq], s_red[(2 * k + 1) * NARROW_HEADS + hq]); };
+
+    // O^T accumulators: dims 128 wave + 32 m + (0..31) of the 32 heads: o[m]
+    f32x16 o[4];
+    for (int pass = 0;; ++pass) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) o[m] = f32x16{};
+        l_lane = 0.0f;
+        s_max = -INFINITY;
+        first_tile = pass == 0;
+        for (int c = 0; c < nchunks; ++c) {
+            // a one-chunk list keeps its row list for the second pass
+            if (pass == 0 || nchunks > 1) resolve_chunk(c, pass == 0 && c == 0);
+            // The index loads have completed (the row list is built); Q's may
+            // still be in flight: they are older than the gathers, so the tile
+            // loop's in-order waits for a tile's gathers cover them too.
+            if (ntiles > 0) issue_rows(load_rows(0), slot(0));
+            if (ntiles > 1) issue_rows(load_rows(1), slot(1));
+            GatherRows gnext;
+            if (ntiles > 2) gnext = load_rows(2);
+            for (int it = 0; it < ntiles; ++it) {
+                // tile it landed (tile it+1 may be in flight); after the barrier
+                // every wave is done with tile it-1 (its slot receives tile it+2)
+                // and with its P
+                if (it + 1 < ntiles) wait_vm<LPW>();
+                else wait_vm<0>();
+                tile_barrier();
+                const lds_ptr kt = slot(it % 3);
+                // the gathers of tile it+2, into the slot of tile it-1
+                __builtin_amdgcn_sched_barrier(0);
+                if (it + 2 < ntiles) issue_rows(gnext, slot((it + 2) % 3));
+                __builtin_amdgcn_sched_barrier(0);
+                f32x4 s = qk16(kt);
+                // ---- V^T operands of PV (transposed reads): 16-lane group g16
+                // reads rows R..R+3 (lane 4rr+pp: row R+rr, dims d0+4pp..+3) with
+                // R = 16u + 4hi and R + 8 ----
+                const int vln = opaque(lane);
+                const int vhi = vln >> 5;
+                const int g16 = vln >> 4, i16 = vln & 15, vrr = i16 >> 2, vpp = i16 & 3;
+                const int vx = 2 * (g16 & 1) + (vpp >> 1);
+                const lds_cptr v_a = kt + (4 * vhi + vrr) * NOPE_STRIDE + 16 * (vx ^ vhi) + 8 * (vpp & 1) + 256 * wave;
+                const lds_cptr v_b =
+                    kt + (4 * vhi + vrr + 8) * NOPE_STRIDE + 16 * (vx ^ (vhi + 2)) + 8 * (vpp & 1) + 256 * wave;
+                auto v_frag = [&](int u, int m) -> u32x4 {
+                    const s16x4 va = lds_read_tr16(v_a + 16 * u * NOPE_STRIDE + 64 * m);
+                    const s16x4 vb = lds_read_tr16(v_b + 16 * u * NOPE_STRIDE + 64 * m);
+                    return __builtin_bit_cast(u32x4, __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7));
+                };
+                const int rows_left = n_valid - it * TILE;
+                const int row0 = 16 * rb + 4 * g4;
+                if (first_tile) {
+                    // the reference: the largest score of the list's first tile
+                    float mx = -INFINITY;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, row0 + i < rows_left ? s[i] : -INFINITY);
+                    put_half(0, red4_max(mx));
+                    tile_barrier();
+                    m_ref = get_max(0) * c_s;
+                    first_tile = false;
+                }
+                if (rows_left < TILE) {
+                    asm volatile("");
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) s[i] = row0 + i < rows_left ? s[i] : -INFINITY;
+                }
+                s_max = fmaxf(s_max, fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+                if (nchunks == 1 && ntiles == 1) {
+                    // single-tile list: the exact sum folded into the reference,
+                    // so that P is normalised when it is rounded
+                    // (opus_attn/dsa_v32/common/host.cc:448-451)
+                    float lt = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) lt += __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], c_s, -m_ref));
+                    put_half(1, red4_sum(lt));
+                    tile_barrier();
+                    m_ref += __builtin_amdgcn_logf(s_red[2 * NARROW_HEADS + hq] + s_red[3 * NARROW_HEADS + hq]);
+                }
+                f32x4 e;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], c_s, -m_ref));
+                l_lane += (e[0] + e[1]) + (e[2] + e[3]);
+                // P of rows 16 rb + 4 g4 + i: PV k-step u = rb, lane half g4 & 1,
+                // positions 4 (g4 >> 1) + i (the rows the V reads pair with them)
+                lds_st<u32x2>(PX + ((2 * rb + (g4 & 1)) * NARROW_HEADS + hq) * 16 + 8 * (g4 >> 1),
+                              __builtin_bit_cast(u32x2, __builtin_convertvector(e, bf16x4)));
+                tile_barrier();
+                // ---- O^T[128 dims of this wave x 32 heads] += V^T P^T ----
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const u32x4 pb = lds_ld<u32x4>(PX + ((2 * u + vhi) * NARROW_HEADS + (vln & 31)) * 16);
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) o[m] = mfma_bf16(v_frag(u, m), pb, o[m]);
+                }
+                if (it + 3 < ntiles) gnext = load_rows(it + 3);
+            }
+            // drain in-flight gathers before the slots can be reused or left
+            wait_vm<0>();
+        }
+        // per head: the largest score of the pass over both row halves (log2
+        // units); NaN compares false.  A head past the reference by more than
+        // TAU restarts the workgroup once, with the exact maximum.
+        put_half(2, red4_max(s_max));
+        // (the barrier also ends every wave's use of the tile buffers: a
+        // restart refills them, the epilogue stages O in them)
+        tile_barrier();
+        const float top = get_max(2) * c_s;
+        if (pass == 0 && __builtin_amdgcn_ballot_w64(top - m_ref > Lay<DSA_KV_BF16>::TAU) != 0 && lane == 0)
+            s_misc[NWAVE] = 1;
+        tile_barrier();
+        if (pass != 0 || s_misc[NWAVE] == 0) break;
+        m_ref = fmaxf(m_ref, top);
+    }
+
+    // ---- epilogue: O / l and LSE, final (bf16) or a split's partial (fp32) ----
+    // the sums and references per head, from the QK^T lanes to the PV lanes (head r32)
+    put_half(3, red4_sum(l_lane));
+    if (rb == 0 && g4 == 0) s_red[8 * NARROW_HEADS + hq] = m_ref;
+    tile_barrier();
+    const float l = s_red[6 * NARROW_HEADS + r32] + s_red[7 * NARROW_HEADS + r32];
+    const float m_fin = s_red[8 * NARROW_HEADS + r32];
+    const bool has = any_rows;
+    // (a cut list: NaN outputs, never a silently truncated attention)
+    const float inv = truncated ? __builtin_nanf("") : (has ? (nchunks == 1 && ntiles == 1 ? 1.0f : 1.0f / l) : 0.0f);
+    const int64_t qrow = (int64_t)b * p.s_q + t;
+    const bool to_part = p.part_o != nullptr;
+    const int64_t part_row = (int64_t)split * p.B * p.s_q + qrow;
+    if (wave == 0 && hi == 0 && head_g < p.H) {
+        const float lse_v = truncated ? __builtin_nanf("") : (m_fin + __builtin_amdgcn_logf(l)) * LN2;
+        if (!to_part) {
+            if (p.lse) p.lse[qrow * p.H + head_g] = has || truncated ? lse_v : INFINITY;
+        } else {
+            p.part_lse[part_row * p.H + head_g] = has || truncated ? lse_v : -FLT_MAX;
+        }
+    }
+    // lane (hi, r32), reg 4g + i of o[m]: dim 128 wave + 32 m + 8 g + 4 hi + i of head r32.
+    // Staged through LDS (each wave its own region) so that the global stores
+    // write whole row pieces of the wave's 128 dims.
+    const int ln = opaque(lane);
+    if (!to_part) {
+        constexpr int OST = 2 * 128 + 16;               // staged head row: 128 bf16 + pad
+        static_assert(NWAVE * 32 * OST <= TILE_BYTES, "O stage fits a tile buffer");
+        const lds_ptr stg = TB + wave * 32 * OST;
+        const int st_w = opaque(r32 * OST + 8 * hi);
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 v4 = {o[m][4 * g] * inv, o[m][4 * g + 1] * inv, o[m][4 * g + 2] * inv,
+                                  o[m][4 * g + 3] * inv};
+                lds_st<u32x2>(stg + st_w + 2 * (32 * m + 8 * g), __builtin_bit_cast(u32x2, __builtin_convertvector(v4, bf16x4)));
+            }
+        __bf16* const orow = p.out + (int64_t)b * p.o_sb + (int64_t)t * p.o_st;
+        const bool o16 = ((p.o_sb | p.o_st | p.o_sh) & 7) == 0 && ((uintptr_t)p.out & 15) == 0;
+        // lane (k, c): head row 4k + c / 16 of the group, dims 8 (c % 16) .. +7 of the wave's 128
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int r = 4 * k + (ln >> 4);
+            if (hbase + r >= p.H) break;
+            const u32x4 v = lds_ld<u32x4>(stg + r * OST + 16 * (ln & 15));
+            __bf16* const dst = orow + (int64_t)(hbase + r) * p.o_sh + 128 * wave + 8 * (ln & 15);
+            if (o16) {
+                *reinterpret_cast<u32x4*>(dst) = v;
+            } else {
+                reinterpret_cast<u32x2*>(dst)[0] = u32x2{v[0], v[1]};
+                reinterpret_cast<u32x2*>(dst)[1] = u32x2{v[2], v[3]};
+            }
+        }
+    } else {
+        constexpr int PST = 4 * 128 + 16;               // staged head row: 128 floats + pad
+        static_assert(2 * 32 * PST <= TILE_BYTES, "two waves' partial stages fit a tile buffer");
+        const lds_ptr stg = TB + (wave >> 1) * TILE_BYTES + (wave & 1) * 32 * PST;
+        const int st_w = opaque(r32 * PST + 16 * hi);
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 v4 = {o[m][4 * g] * inv, o[m][4 * g + 1] * inv, o[m][4 * g + 2] * inv,
+                                  o[m][4 * g + 3] * inv};
+                lds_st<f32x4>(stg + st_w + 4 * (32 * m + 8 * g), v4);
+            }
+        const int64_t prow0 = part_row * p.H + hbase;
+        // lane (j, c): head row 2k + j of the group, floats 4c..4c+3 of the wave's 128
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int r = 2 * k + (ln >> 5);
+            const f32x4 v = lds_ld<f32x4>(stg + r * PST + 16 * (ln & 31));
+            if (hbase + r < p.H)
+                *reinterpret_cast<f32x4*>(p.part_o + (prow0 + r) * D_VO + 128 * wave + 4 * (ln & 31)) = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Split combine: one wave per (row, head); lane holds 8 of the 512 outputs.
 // Math of mla_reduce (opus_attn/dsa_v32/common/mla_reduce.hpp:6-156):
 // m = max lse_i, w_i = exp(lse_i - m) (0 for an empty split),
@@ -1937,6 +2450,16 @@ bool heads_ok(int32_t H, int64_t tokens) {
     return H >= 1 && tokens * head_groups(H) <= INT32_MAX;
 }
 
+// 32-head workgroups (dsa_mla_fwd_narrow_kernel) for bf16 576-value rows in
+// the top-k form: when a query token's 128-head workgroup would be mostly
+// padding heads (H <= 64), or when the 128-head workgroups are too few to
+// occupy the GPU without many splits (fewer than 64).
+int narrow_groups(int32_t H) { return (H + NARROW_HEADS - 1) / NARROW_HEADS; }
+bool narrow_path(int fmt, int64_t tokens, int32_t H) {
+    if (fmt != DSA_KV_BF16 || H < 1 || tokens * narrow_groups(H) > INT32_MAX) return false;
+    return H <= 64 || tokens * head_groups(H) < 64;
+}
+
 int auto_splits(int64_t queries, int topk) {
     int ns = 1;
     if (queries > 0 && queries < 256) {
@@ -1958,7 +2481,9 @@ int validate_decode(const dsa_mla_decode_args* a, int* ns_out, int* chunk_out) {
     if (a->block_table && a->block_size <= 0) return DSA_ERR_BAD_SHAPE;
     if (row_stride_bytes(a->kv_format, a->kv_stride_row) < 0) return DSA_ERR_BAD_STRIDE;
     if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
-    const int ns = a->num_splits ? a->num_splits : auto_splits((int64_t)a->B * a->s_q * head_groups(a->H), a->topk);
+    const int64_t tokens = (int64_t)a->B * a->s_q;
+    const int64_t wgs = tokens * (narrow_path(a->kv_format, tokens, a->H) ? narrow_groups(a->H) : head_groups(a->H));
+    const int ns = a->num_splits ? a->num_splits : auto_splits(wgs, a->topk);
     const int chunk = a->topk == 0 ? 0 : (a->topk + ns - 1) / ns;
     if (a->B > 0 && a->topk > 0) {
         if (!a->q || !a->kv_cache || !a->seq_lens || !a->indices || !a->out) return DSA_ERR_NULL_POINTER;
@@ -1982,9 +2507,10 @@ size_t decode_ws_bytes(const dsa_mla_decode_args* a, int ns) {
     return (size_t)ns * rows * (D_VO + 1) * sizeof(float) + 256;
 }
 
-int launch_fwd(const FwdParams& fp, int fmt, int B, int s_q, int ns, hipStream_t st) {
+int launch_fwd(const FwdParams& fp, int fmt, int B, int s_q, int ns, hipStream_t st, bool narrow = false) {
     dim3 grid((unsigned)((int64_t)B * fp.hgroups), s_q, ns), block(NTHR);
-    if (fmt == DSA_KV_BF16) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_BF16>, grid, block, 0, st, fp);
+    if (narrow) hipLaunchKernelGGL(dsa_mla_fwd_narrow_kernel, grid, block, 0, st, fp);
+    else if (fmt == DSA_KV_BF16) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_BF16>, grid, block, 0, st, fp);
     else if (fmt == DSA_KV_FP8_656) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_FP8_656>, grid, block, 0, st, fp);
     else if (fmt == DSA_KV_MXFP8) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_MXFP8>, grid, block, 0, st, fp);
     else if (fmt == DSA_KV_MXFP8_V4) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_MXFP8_V4>, grid, block, 0, st, fp);
@@ -2153,7 +2679,8 @@ size_t prefill_ws_bytes(int ns, int64_t N, int H) {
 }
 // Forward kernel over ns splits of N query tokens, then (ns > 1) the combine of
 // their partials, with the attention sink folded in once by the combine.
-int prefill_launch(FwdParams& fp, int fmt, int ns, const float* sink, void* ws, hipStream_t st) {
+int prefill_launch(FwdParams& fp, int fmt, int ns, const float* sink, void* ws, hipStream_t st,
+                   bool narrow = false) {
     const int64_t N = fp.B;
     if (ns > 1) {
         fp.part_o = (float*)ws;
@@ -2162,7 +2689,7 @@ int prefill_launch(FwdParams& fp, int fmt, int ns, const float* sink, void* ws, 
     } else {
         fp.attn_sink = sink;
     }
-    const int r = launch_fwd(fp, fmt, (int)N, 1, ns, st);
+    const int r = launch_fwd(fp, fmt, (int)N, 1, ns, st, narrow);
     if (r || ns == 1) return r;
     return launch_combine(fp.part_o, fp.part_lse, ns, (int)N, fp.H, 1, fp.out, fp.o_sb, 0, fp.o_sh, fp.lse, st,
                           sink);
@@ -2176,7 +2703,9 @@ int validate_prefill(const dsa_mla_prefill_args* a, int* ns_out) {
     if (row_stride_bytes(a->kv_format, a->kv_stride_row) < 0) return DSA_ERR_BAD_STRIDE;
     if (a->topk > MAX_LIST) return DSA_ERR_BAD_SHAPE;
     if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
-    *ns_out = prefill_splits(a->num_splits, (int64_t)a->N * head_groups(a->H), a->topk);
+    const bool narrow = narrow_path(a->kv_format, a->N, a->H);
+    *ns_out = prefill_splits(a->num_splits, (int64_t)a->N * (narrow ? narrow_groups(a->H) : head_groups(a->H)),
+                             a->topk);
     if (a->N == 0) return DSA_OK;
     if (!a->q || !a->out || (a->topk > 0 && (!a->kv || !a->indices))) return DSA_ERR_NULL_POINTER;
     if ((a->q_stride_n % 8) || (a->q_stride_h % 8) || (a->o_stride_n % 4) || (a->o_stride_h % 4))
@@ -2313,9 +2842,10 @@ int dsa_mla_decode_noalloc(const dsa_mla_decode_args* a, void* stream) {
 namespace {
 
 int decode_launch(const dsa_mla_decode_args* a, int ns, int chunk, void* ws, hipStream_t st) {
+    const bool narrow = narrow_path(a->kv_format, (int64_t)a->B * a->s_q, a->H);
     FwdParams fp{};
     fp.H = a->H;
-    fp.hgroups = head_groups(a->H);
+    fp.hgroups = narrow ? narrow_groups(a->H) : head_groups(a->H);
     fp.q = (const __bf16*)a->q;
     fp.q_sb = a->q_stride_b; fp.q_st = a->q_stride_t; fp.q_sh = a->q_stride_h;
     fp.kv = (const unsigned char*)a->kv_cache;
@@ -2342,7 +2872,7 @@ int decode_launch(const dsa_mla_decode_args* a, int ns, int chunk, void* ws, hip
         fp.part_o = (float*)ws;
         fp.part_lse = (float*)((char*)ws + (size_t)ns * rows * D_VO * sizeof(float));
     }
-    int r = launch_fwd(fp, a->kv_format, a->B, a->s_q, ns, st);
+    int r = launch_fwd(fp, a->kv_format, a->B, a->s_q, ns, st, narrow);
     if (r || ns == 1) return r;
     return launch_combine(fp.part_o, fp.part_lse, ns, a->B * a->s_q, a->H, a->s_q, a->out, a->o_stride_b,
                           a->o_stride_t, a->o_stride_h, a->lse, st);
@@ -2379,9 +2909,11 @@ int dsa_mla_decode_csr(const dsa_mla_decode_csr_args* a, void* ws, size_t ws_byt
     if (need && (!ws || ws_bytes < need || ((uintptr_t)ws & 15))) return DSA_ERR_WORKSPACE;
     if (a->B == 0) return DSA_OK;
     hipStream_t st = (hipStream_t)stream;
+    // uniform splits (no work plan) of few query rows or few heads: 32-head workgroups
+    const bool narrow = ns >= 1 && narrow_path(a->kv_format, (int64_t)a->B * a->s_q, a->H);
     FwdParams fp{};
     fp.H = a->H;
-    fp.hgroups = head_groups(a->H);
+    fp.hgroups = narrow ? narrow_groups(a->H) : head_groups(a->H);
     fp.q = (const __bf16*)a->q;
     fp.q_sb = (int64_t)a->s_q * a->stride_q_b; fp.q_st = a->stride_q_b; fp.q_sh = a->stride_q_h;
     fp.kv = (const unsigned char*)a->kv;
@@ -2402,7 +2934,7 @@ int dsa_mla_decode_csr(const dsa_mla_decode_csr_args* a, void* ws, size_t ws_byt
         fp.part_o = (float*)ws;
         fp.part_lse = (float*)((char*)ws + (size_t)ns * rows * D_VO * sizeof(float));
     }
-    int r = launch_fwd(fp, a->kv_format, a->B, a->s_q, ns, st);
+    int r = launch_fwd(fp, a->kv_format, a->B, a->s_q, ns, st, narrow);
     if (r || ns == 1) return r;
     return launch_combine(fp.part_o, fp.part_lse, ns, a->B * a->s_q, a->H, a->s_q, a->out, fp.o_sb, fp.o_st,
                           fp.o_sh, a->lse, st);
@@ -2486,9 +3018,10 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* a, void* ws, size_t ws_bytes, vo
     const size_t need = prefill_ws_bytes(ns, a->N, a->H);
     if (need && (!ws || ws_bytes < need || ((uintptr_t)ws & 15))) return DSA_ERR_WORKSPACE;
     if (a->N == 0) return DSA_OK;
+    const bool narrow = narrow_path(a->kv_format, a->N, a->H);
     FwdParams fp{};
     fp.H = a->H;
-    fp.hgroups = head_groups(a->H);
+    fp.hgroups = narrow ? narrow_groups(a->H) : head_groups(a->H);
     fp.q = (const __bf16*)a->q;
     fp.q_sb = a->q_stride_n; fp.q_st = 0; fp.q_sh = a->q_stride_h;
     fp.kv = (const unsigned char*)a->kv;
@@ -2511,7 +3044,7 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* a, void* ws, size_t ws_bytes, vo
     fp.causal_offset = a->causal_offset;
     fp.reverse = 1;
     fp.scale_log2 = a->sm_scale * LOG2E;
-    return prefill_launch(fp, a->kv_format, ns, nullptr, ws, (hipStream_t)stream);
+    return prefill_launch(fp, a->kv_format, ns, nullptr, ws, (hipStream_t)stream, narrow);
 }
 
 int dsa_mla_prefill_v4_workspace_size(const dsa_mla_prefill_v4_args* a, size_t* bytes) {

@@ -52,18 +52,33 @@ __host__ __device__ inline int32_t csr_row(int32_t j, int64_t rows) {
 // log2(block_size) for a power of two, else -1).  Flat (bt_row == NULL):
 // flat_base + j.  A physical row outside [0, rows) is skipped, so a bad
 // block table cannot address memory outside the cache.
-__host__ __device__ inline int64_t topk_row(int32_t j, int64_t jmax, const int32_t* bt_row, int32_t block_size,
-                                            int32_t bs_shift, int64_t flat_base, int64_t rows) {
+//
+// The rule in two steps, so that a caller resolving several entries can
+// issue all their block-table reads before it waits for any: topk_block()
+// gives the block-table slot of position j (-1: j is skipped), topk_finish()
+// the row from that slot's entry (read only when paged).
+__host__ __device__ inline int32_t topk_block(int32_t j, int64_t jmax, int32_t block_size, int32_t bs_shift) {
     if (j < 0 || (int64_t)j >= jmax) return -1;
+    return bs_shift >= 0 ? (j >> bs_shift) : (j / block_size);
+}
+__host__ __device__ inline int64_t topk_finish(int32_t j, int32_t blk_i, int32_t bt_entry, bool paged,
+                                               int32_t block_size, int32_t bs_shift, int64_t flat_base,
+                                               int64_t rows) {
+    if (blk_i < 0) return -1;
     int64_t row;
-    if (bt_row) {
-        const int32_t blk_i = bs_shift >= 0 ? (j >> bs_shift) : (j / block_size);
+    if (paged) {
         const int32_t in_blk = bs_shift >= 0 ? (j & (block_size - 1)) : (j % block_size);
-        row = (int64_t)bt_row[blk_i] * block_size + in_blk;
+        row = (int64_t)bt_entry * block_size + in_blk;
     } else {
         row = flat_base + j;
     }
     return row >= 0 && row < rows ? row : -1;
+}
+__host__ __device__ inline int64_t topk_row(int32_t j, int64_t jmax, const int32_t* bt_row, int32_t block_size,
+                                            int32_t bs_shift, int64_t flat_base, int64_t rows) {
+    const int32_t blk = topk_block(j, jmax, block_size, bs_shift);
+    return topk_finish(j, blk, bt_row && blk >= 0 ? bt_row[blk] : 0, bt_row != nullptr, block_size, bs_shift,
+                       flat_base, rows);
 }
 
 }  // namespace dsa_rows

@@ -562,13 +562,18 @@ def _prefill_ws(lib, fn, a):
 def test_prefill_split_workspace(lib):
     """Split-K prefill: automatic splits only when fewer than 256 workgroups would run (at
     least 256 list entries per split), the workspace holding num_splits x N x H x 513 floats;
-    explicit counts 1..64; a missing or short workspace is rejected before any launch."""
+    explicit counts 1..64; a missing or short workspace is rejected before any launch.
+    Workgroups per query: 4 (32-head groups) for bf16 rows with fewer than 64 queries of
+    H = 128, else 1 (128 heads)."""
     per = 128 * 513 * 4
     # C5-sized: 8192 queries, unsplit, no workspace
     assert _prefill_ws(lib, lib.dsa_mla_prefill_workspace_size, _prefill_args()) == (0, 0)
-    # 16 queries of a 65536-entry list: 16 splits
+    # 16 queries of a 65536-entry list (64 workgroups of 32 heads): 4 splits
     rc, n = _prefill_ws(lib, lib.dsa_mla_prefill_workspace_size, _prefill_args(N=16, topk=65536))
-    assert rc == 0 and n == 16 * 16 * per + 256
+    assert rc == 0 and n == 4 * 16 * per + 256
+    # 64 queries: 128-head workgroups, 4 splits
+    rc, n = _prefill_ws(lib, lib.dsa_mla_prefill_workspace_size, _prefill_args(N=64, topk=65536))
+    assert rc == 0 and n == 4 * 64 * per + 256
     # short lists keep >= 256 entries per split
     rc, n = _prefill_ws(lib, lib.dsa_mla_prefill_workspace_size, _prefill_args(N=16, topk=600))
     assert rc == 0 and n == 2 * 16 * per + 256
