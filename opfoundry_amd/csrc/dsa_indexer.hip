@@ -176,28 +176,27 @@ dsa_indexer_kernel(const IxParams p) {
         }
         // ---- epilogue: lane (r32, hi) has position 32w + r32 of the chunk, and
         // in register r of row block qb the row 32qb + 8(r/4) + 4hi + r%4 ----
-        float part[TPW];
-#pragma unroll
-        for (int tk = 0; tk < TPW; ++tk) part[tk] = 0.0f;
-#pragma unroll
-        for (int qb = 0; qb < 4; ++qb) {
-            const int tk = 32 * qb / HI;
-#pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                const f32x4 wv = lds_ld<f32x4>((lds_cptr)s_w + 4 * (32 * qb + 8 * r4 + 4 * hi));
-#pragma unroll
-                for (int e = 0; e < 4; ++e) part[tk] += wv[e] * fmaxf(acc[qb][4 * r4 + e], 0.0f);
-            }
-        }
         const int pl = c * IX_CHUNK + 32 * wave + r32;    // position within the span
         const int64_t j = span0 + pl;
         const bool bad = s_rows[pl] < 0;
+        // token tk: row blocks tk * HI / 32 .. (tk + 1) * HI / 32 - 1, one token
+        // at a time (few values live beside Q and the accumulators)
 #pragma unroll
         for (int tk = 0; tk < TPW; ++tk) {
-            part[tk] += __shfl_xor(part[tk], 32, 64);
+            float part = 0.0f;
+#pragma unroll
+            for (int qb = tk * HI / 32; qb < (tk + 1) * HI / 32; ++qb) {
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const f32x4 wv = lds_ld<f32x4>((lds_cptr)s_w + 4 * (32 * qb + 8 * r4 + 4 * hi));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) part += wv[e] * fmaxf(acc[qb][4 * r4 + e], 0.0f);
+                }
+            }
+            part += __shfl_xor(part, 32, 64);
             // token tk's score leaves through the lanes of half (tk & 1)
             if ((tk & 1) == hi && tk < ntok && j < s_len[tk])
-                p.scores[((int64_t)b * p.s_q + t0 + tk) * p.s_stride + j] = bad ? -INFINITY : part[tk];
+                p.scores[((int64_t)b * p.s_q + t0 + tk) * p.s_stride + j] = bad ? -INFINITY : part;
         }
         tile_barrier();                    // every wave done with buffer c&1
     }

@@ -52,6 +52,13 @@ __device__ __forceinline__ int opaque(int v) {
     asm("" : "+v"(v));
     return v;
 }
+// The same as volatile asm, which is never merged with another copy: values
+// derived from it are computed where they are used, so a one-off epilogue does
+// not keep a prologue value alive across the tile loop.
+__device__ __forceinline__ int opaque_here(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
 
 // 16-byte LDS-DMA load: lane l's 16 bytes from gsrc land at lds_wave_base +
 // 16*l.  Issued through inline asm so the compiler neither waits on it at the

@@ -451,7 +451,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         // B operand of the scaled fp8 MFMA (64-deep k-steps k8): lane (head,
         // hi) holds codes 64 k8 + 16 hi .. +15 and 64 k8 + 32 + 16 hi .. +15,
         // in qf[2 k8] and qf[2 k8 + 1]; RoPE as bf16 in qf[KS_NOPE ..]
-        const unsigned char* q8p = p.q8 + (int64_t)b * p.q8_sb + (int64_t)t * p.q8_st + (int64_t)head_q * p.q8_sh + 16 * hi;
+        // (the lane offset from a fresh copy of the lane id: shared with the
+        // epilogue's, it stayed live across the tile loop and spilled)
+        const unsigned char* q8p = p.q8 + (int64_t)b * p.q8_sb + (int64_t)t * p.q8_st + (int64_t)head_q * p.q8_sh +
+                                   16 * (opaque_here(lane) >> 5);
 #pragma unroll
         for (int k8 = 0; k8 < KS_NOPE / 4; ++k8) {
             qf[2 * k8] = *reinterpret_cast<const u32x4*>(q8p + 64 * k8);
@@ -1537,7 +1540,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         static_assert(32 * OUT_STRIDE <= TILE_BYTES, "O stage fits a tile buffer");
         __bf16* const orow = p.out + (int64_t)b * p.o_sb + (int64_t)t * p.o_st;
         // per-lane stage offsets, computed here (not hoisted into the tile loop)
-        const int ln = opaque(lane);
+        const int ln = opaque_here(lane);
         const int st_w = opaque(r32 * OUT_STRIDE + 2 * d0);
         // 16-byte stores need 16-byte aligned rows; the API allows 8
         const bool o16 = ((p.o_sb | p.o_st | p.o_sh) & 7) == 0 && ((uintptr_t)p.out & 15) == 0;
@@ -1580,7 +1583,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         // reads and the next head block's writes.
         constexpr int PST = D_VO + 16;        // bytes per staged head row: 128 floats + pad
         static_assert(2 * 32 * PST <= TILE_BYTES, "two waves' partial stages fit a tile buffer");
-        const int ln = opaque(lane);
+        const int ln = opaque_here(lane);
         const lds_ptr stg = (wave < 2 ? T0 : T1) + (wave & 1) * 32 * PST;
         const int st_w = opaque(r32 * PST + 16 * hi);
         const int64_t prow0 = part_row * p.H + hbase;
