@@ -43,6 +43,16 @@ BF16_PEAK_TFLOPS = 2500.0
 SM_SCALE = 1.0 / math.sqrt(192.0)
 FLOP_PER_PAIR = 2 * H * (D_QK + D_VO)
 
+
+def bf16_fwd_kernel(tokens, splits, heads=H, d512=False):
+    """Name of the forward kernel the library runs for bf16 rows: 32-head workgroups when
+    heads <= 32 or when the 128-head kernel would run fewer than 128 workgroups, else the
+    128-head one.  (splits: the 128-head kernel's split count.)"""
+    narrow = heads <= 32 or tokens * ((heads + 127) // 128) * splits < 128
+    if narrow:
+        return "dsa_mla_fwd_narrow_kernel<" + ("512" if d512 else "576") + ">"
+    return "dsa_mla_fwd_kernel<" + ("bf16_d512" if d512 else "bf16") + ">"
+
 CONFIGS = {
     "c1": dict(kind="decode", B=2, s_q=1, seq=8192, block=None, topk=2048, pad=256, fp8=False,
                causal=False),
@@ -717,8 +727,8 @@ def decode_leg(name, args, dev, dst):
            "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(ach / HBM_PEAK_GBS, 4),
                         "traffic": profiled_traffic(f"dsa_mla_fwd_bf16_{name}_traffic.txt"),
-                        "kernel": "dsa_mla_fwd_kernel<bf16>" + (" + dsa_mla_combine_kernel (whole step)"
-                                                                 if ns > 1 else ""),
+                        "kernel": bf16_fwd_kernel(T, ns) + (" + dsa_mla_combine_kernel (whole step)"
+                                                        if ns > 1 else ""),
                         "kernel_avg_us": round(ms * 1e3, 3), "alg_bytes": alg_bytes,
                         "mfma_frac": round(FLOP_PER_PAIR * V / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)},
            "reference_figures": reference_figures(T, s_q, V, row_bytes, ms)}
@@ -1220,6 +1230,31 @@ def c5_leg(args, dev, res):
                                    "kernel_avg_us": round(pk_ms * 1e3, 1)}}
     defer_cpu(args, "CPU baseline (oracle) on a c5 sample", res["prefill"],
               lambda: cpu_baseline_prefill(p, args.cpu_prefill_sample, pV))
+    # The c5 lists with fewer heads (the first H heads of c5's Q): H <= 32 runs on 32-head
+    # workgroups, H = 64 on 128-head ones; the fraction is of useful flops (H heads).
+    import torch
+    from opfoundry_amd import dsa
+    res["prefill_heads"] = {}
+    for Hs in (16, 32, 64):
+        qh = p["q"][:, :Hs].contiguous()
+        hout = torch.empty((qh.shape[0], Hs, D_VO), dtype=torch.bfloat16, device=dev)
+        hlse = torch.empty((qh.shape[0], Hs), dtype=torch.float32, device=dev)
+        a = dsa.make_prefill_args(qh, p["kv"], p["idx"], SM_SCALE, hout, hlse)
+        nb = dsa.prefill_workspace_size(a)
+        hws = torch.empty(nb, dtype=torch.uint8, device=dev) if nb else None
+        hstep = prepared_prefill(a, hws)
+        hms = time_steps(hstep, psteps, args.warmup)
+        hfl = pfl * Hs / H
+        res["prefill_heads"][f"H{Hs}"] = {
+            "workload": f"c5 lists, H={Hs}", "ms_per_step": round(hms, 4),
+            "tflops": round(hfl / (hms * 1e-3) / 1e12, 1),
+            "vs_c5_time": round(hms / pms, 3), "ideal_vs_c5_time": round(Hs / H, 3),
+            "roofline": {"bound": "mfma", "achieved": round(hfl / (hms * 1e-3) / 1e12, 1),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(hfl / (hms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                         "traffic": None, "kernel": bf16_fwd_kernel(qh.shape[0], 1, heads=Hs),
+                         "kernel_avg_us": round(hms * 1e3, 1)}}
+        del hws, hout, hlse
 
 
 def mx_leg(args, dev, res):
@@ -1266,7 +1301,7 @@ def v4_leg(name, args, dev, dst):
                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(vfl / (vms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
                         "traffic": profiled_traffic(f"dsa_mla_fwd_{name}_traffic.txt"),
-                        "kernel": "dsa_mla_fwd_kernel<mxfp8_v4>" if v["fp8"] else "dsa_mla_fwd_kernel<bf16_d512>",
+                        "kernel": "dsa_mla_fwd_kernel<mxfp8_v4>" if v["fp8"] else bf16_fwd_kernel(v["N"], 1, d512=True),
                         "kernel_avg_us": round(vms * 1e3, 1)}}
     del keep
     defer_cpu(args, f"CPU baseline (oracle) on a {name} sample", leg,
@@ -1300,7 +1335,7 @@ def v4_split_leg(name, args, dev, dst):
         "tflops": round(tf, 1),
         "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": ("dsa_mla_fwd_kernel<mxfp8_v4>" if v["fp8"] else "dsa_mla_fwd_kernel<bf16_d512>")
+                     "kernel": ("dsa_mla_fwd_kernel<mxfp8_v4>" if v["fp8"] else bf16_fwd_kernel(v["N"], ns, d512=True))
                                + " + dsa_mla_combine_kernel (whole step)",
                      "kernel_avg_us": round(t["split"] * 1e3, 1)}}
 

@@ -1612,8 +1612,9 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Narrow forward kernel (bf16 576-value rows; top-k form, or CSR form with
-// uniform splits): one workgroup per (query token, group of 32 heads, split).
+// Narrow forward kernel (bf16 rows: 576-value rows in the top-k form or the
+// CSR form with uniform splits, or the V4 prefill's 512-value rows): one
+// workgroup per (query token, group of 32 heads, split).
 // For few query tokens (low-batch decode) and small head counts: a 128-head
 // workgroup per token leaves most CUs idle, or computes padding heads, while
 // 32-head groups give 4x the workgroups, each with a quarter of the Q load, of
@@ -1630,7 +1631,6 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 // grid = (B * ceil(H / 32), s_q, num_splits), block = 256.
 // ---------------------------------------------------------------------------
 constexpr int NARROW_HEADS = 32;
-constexpr int NKS = D_QK / 32;                // 32-deep k-steps of QK^T (16 NoPE, 2 RoPE)
 constexpr int P_BYTES = 2 * 2 * 32 * 16;      // P of a tile: [u][hi][head] x 8 bf16
 
 __device__ __forceinline__ f32x4 mfma16_bf16(u32x4 a, u32x4 b, f32x4 c) {
@@ -1653,8 +1653,11 @@ __device__ __forceinline__ int32_t sload(const int32_t* ptr) {
     return *(const __attribute__((address_space(4))) int32_t*)(uintptr_t)ptr;
 }
 
+template <bool D512>
 __global__ void __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(1, 1)))
 dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
+    // 32-deep k-steps of QK^T: 16 NoPE + 2 RoPE, or the 16 of a 512-value row
+    constexpr int NKS = (D512 ? D_NOPE : D_QK) / 32;
     __shared__ __attribute__((aligned(1024))) unsigned char s_tiles[3 * TILE_BYTES];
     __shared__ __attribute__((aligned(16))) unsigned char s_p[P_BYTES];
     __shared__ int32_t s_rows_arr[MAX_CHUNK];
@@ -1683,6 +1686,16 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
                    "+s"(p.idx_st), "+s"(p.s_q), "+s"(p.topk), "+s"(p.chunk), "+s"(p.H), "+s"(p.hgroups),
                    "+s"(p.causal), "+s"(p.causal_offset), "+s"(p.reverse), "+s"(a_o), "+s"(p.o_sb), "+s"(p.o_st),
                    "+s"(p.o_sh), "+s"(a_lse), "+s"(a_po), "+s"(a_pl));
+    if constexpr (D512) {
+        uintptr_t a_np = (uintptr_t)p.ind_pre, a_xp = (uintptr_t)p.idx_pre, a_ne = (uintptr_t)p.ind_ext,
+                  a_xe = (uintptr_t)p.idx_ext, a_sk = (uintptr_t)p.attn_sink;
+        asm volatile("" : "+s"(a_np), "+s"(a_xp), "+s"(a_ne), "+s"(a_xe), "+s"(a_sk), "+s"(p.kv2_rows));
+        p.ind_pre = gptr<const int32_t>(a_np);
+        p.idx_pre = gptr<const int32_t>(a_xp);
+        p.ind_ext = gptr<const int32_t>(a_ne);
+        p.idx_ext = gptr<const int32_t>(a_xe);
+        p.attn_sink = gptr<const float>(a_sk);
+    }
     p.out = gptr<__bf16>(a_o);
     p.lse = gptr<float>(a_lse);
     p.part_o = gptr<float>(a_po);
@@ -1712,12 +1725,28 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
     // ---- this split's entries, by the rules of dsa_mla_fwd_kernel.  Top-k
     // form: logical positions through the block table, bounded by seq_len and
     // the causal rule.  CSR form (uniform splits): physical rows
-    // kv_indices[kv_indptr[b] + k], k below the count-based MTP bound ----
-    const int k0 = split * p.chunk;
+    // kv_indices[kv_indptr[b] + k], k below the count-based MTP bound.  V4
+    // prefill: the prefix rows of kv, then the extend rows of kv2 (POOL2),
+    // at most max_rows of them (a longer list is cut, NaN), the splits taking
+    // whole tiles (opus_attn/dsa_v4/common/mla_prefill_split.h:34-44) ----
+    int k0 = split * p.chunk;
     int k1;
     const int32_t* idx;
     bool truncated = false;
-    if (p.kv_indptr) {
+    int64_t v4_np = 0, v4_eb = 0;
+    if constexpr (D512) {
+        const int64_t pb = sload(p.ind_pre + b);
+        v4_np = max((int64_t)sload(p.ind_pre + b + 1) - pb, (int64_t)0);
+        v4_eb = sload(p.ind_ext + b);
+        const int64_t ne = max((int64_t)sload(p.ind_ext + b + 1) - v4_eb, (int64_t)0);
+        const int64_t n_b = min(v4_np + ne, (int64_t)p.topk);
+        truncated = v4_np + ne > p.topk;
+        const int64_t per = (n_b + grid_z - 1) / grid_z;
+        const int64_t cb = (per + TILE - 1) / TILE * TILE;
+        k0 = (int)min((int64_t)split * cb, n_b);
+        k1 = (int)min((int64_t)k0 + cb, n_b);
+        idx = p.idx_pre + pb;
+    } else if (p.kv_indptr) {
         const int64_t kb = sload(p.kv_indptr + b);
         const int64_t count = (int64_t)sload(p.kv_indptr + b + 1) - kb - (p.s_q - 1 - t);
         k1 = (int)min((int64_t)k0 + p.chunk, count);
@@ -1730,14 +1759,16 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
     }
     const int nchunks = k1 > k0 ? (k1 - k0 + MAX_CHUNK - 1) / MAX_CHUNK : 1;
     constexpr int PER_T = MAX_CHUNK / NTHR;       // entries per thread and chunk
-    // the entries of chunk c (-1 past the split's end)
+    // the entries of chunk c (-1 past the split's end); V4: entry k is an
+    // extend entry from k = v4_np on
     auto load_entries = [&](int c, int32_t (&jv)[PER_T]) {
         const int kc0 = k0 + c * MAX_CHUNK;
         const int kc1 = min(kc0 + MAX_CHUNK, k1);
 #pragma unroll
         for (int e = 0; e < PER_T; ++e) {
             const int k = kc0 + tid * PER_T + e;
-            jv[e] = k < kc1 ? idx[k] : -1;
+            if (D512 && k >= v4_np) jv[e] = k < kc1 ? p.idx_ext[v4_eb + (k - v4_np)] : -1;
+            else jv[e] = k < kc1 ? idx[k] : -1;
         }
     };
     // Chunk 0's entries are loaded before Q: vmcnt counts in order, so the wait
@@ -1756,7 +1787,7 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
     // top-k form: the bound on positions, from seq_len and the causal rule
     // (a scalar load, in flight with the entries and Q)
     int64_t jmax = 0;
-    if (!p.kv_indptr) {
+    if (!D512 && !p.kv_indptr) {
         const int64_t Lq = p.seq_lens ? (int64_t)sload(p.seq_lens + b) : p.seq_len_default;
         jmax = Lq;
         if (p.causal == 1) jmax = min(Lq, Lq - p.s_q + t + 1);
@@ -1781,7 +1812,13 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
             } else {
                 load_entries(c, jv);
             }
-            if (p.kv_indptr) {
+            if constexpr (D512) {
+                const int kc0 = k0 + c * MAX_CHUNK;
+#pragma unroll
+                for (int e = 0; e < PER_T; ++e)
+                    rows_local[e] = kc0 + tid * PER_T + e >= v4_np ? dsa_rows::v4_extend_row(jv[e], p.kv2_rows)
+                                                                   : dsa_rows::v4_prefix_row(jv[e], p.kv_total_rows);
+            } else if (p.kv_indptr) {
 #pragma unroll
                 for (int e = 0; e < PER_T; ++e) rows_local[e] = dsa_rows::csr_row(jv[e], p.kv_total_rows);
             } else {
@@ -1818,8 +1855,9 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
     };
 
     // ---- gather: wave w loads NoPE rows 8w..8w+7 (one 1 KB LDS-DMA load per
-    // row) and the RoPE blocks of those rows (one load); tile layout and
-    // swizzles as in dsa_mla_fwd_kernel ----
+    // row) and the RoPE blocks of those rows (one load; none for 512-value
+    // rows, whose row ids name their pool); tile layout and swizzles as in
+    // dsa_mla_fwd_kernel ----
     struct GatherRows {
         int32_t r[TILE / NWAVE];   // this wave's rows (uniform)
         int32_t rope;              // row of this lane's RoPE chunk
@@ -1843,14 +1881,21 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
 #pragma unroll
         for (int i = 0; i < TILE / NWAVE; ++i) {
             const int r = 8 * wave + i;
-            lds_dma16_s(p.kv + (int64_t)__builtin_amdgcn_readfirstlane(g.r[i]) * p.row_bytes,
-                        16u * (unsigned)(ln ^ nope_sw(r)), tb + r * NOPE_STRIDE);
+            const int32_t id = __builtin_amdgcn_readfirstlane(g.r[i]);
+            const unsigned char* base;
+            if constexpr (D512)
+                base = (dsa_rows::row_in_pool2(id) ? p.kv2 : p.kv) + (int64_t)dsa_rows::row_index(id) * p.row_bytes;
+            else
+                base = p.kv + (int64_t)id * p.row_bytes;
+            lds_dma16_s(base, 16u * (unsigned)(ln ^ nope_sw(r)), tb + r * NOPE_STRIDE);
         }
-        const int r = 8 * wave + (ln >> 3);
-        lds_dma16(p.kv + (int64_t)g.rope * p.row_bytes + 2 * D_NOPE + 16 * ((ln & 7) ^ rope_sw(r)),
-                  tb + ROPE_OFF + 8 * wave * 128);
+        if constexpr (!D512) {
+            const int r = 8 * wave + (ln >> 3);
+            lds_dma16(p.kv + (int64_t)g.rope * p.row_bytes + 2 * D_NOPE + 16 * ((ln & 7) ^ rope_sw(r)),
+                      tb + ROPE_OFF + 8 * wave * 128);
+        }
     };
-    constexpr int LPW = TILE / NWAVE + 1;     // loads per wave per tile
+    constexpr int LPW = TILE / NWAVE + (D512 ? 0 : 1);     // loads per wave per tile
 
     // ---- S^T[16 rows x 16 heads] = K Q^T (A operand: row 16 rb + c16, dims
     // 32 ks + 8 g4 .. +7, i.e. chunk 4 ks + g4 at its swizzled position) ----
@@ -1972,7 +2017,11 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
                     for (int i = 0; i < 4; ++i) lt += __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], c_s, -m_ref));
                     put_half(1, red4_sum(lt));
                     tile_barrier();
-                    m_ref += __builtin_amdgcn_logf(s_red[2 * NARROW_HEADS + hq] + s_red[3 * NARROW_HEADS + hq]);
+                    float l1 = s_red[2 * NARROW_HEADS + hq] + s_red[3 * NARROW_HEADS + hq], m_fold = m_ref;
+                    // (an attention sink joins the sum: mla_v4_host.cc:469-472)
+                    if (D512 && p.attn_sink)
+                        add_sink(l1, m_ref, p.attn_sink[min(hbase + hq, p.H - 1)] * LOG2E, l1, m_fold);
+                    m_ref = m_fold + __builtin_amdgcn_logf(l1);
                 }
                 f32x4 e;
 #pragma unroll
@@ -2015,11 +2064,20 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
     put_half(3, red4_sum(l_lane));
     if (rb == 0 && g4 == 0) s_red[8 * NARROW_HEADS + hq] = m_ref;
     tile_barrier();
-    const float l = s_red[6 * NARROW_HEADS + r32] + s_red[7 * NARROW_HEADS + r32];
-    const float m_fin = s_red[8 * NARROW_HEADS + r32];
+    const float l_rows = s_red[6 * NARROW_HEADS + r32] + s_red[7 * NARROW_HEADS + r32];
+    const float m_head = s_red[8 * NARROW_HEADS + r32];
     const bool has = any_rows;
+    // the softmax denominator: the rows' sum plus an attention sink
+    // (mla_v4_host.cc:469-472; LSE then covers the sink as well)
+    float l = l_rows, m_fin = m_head, o_scale = 1.0f;
+    if constexpr (D512)
+        if (p.attn_sink) {
+            add_sink(l_rows, m_head, p.attn_sink[min(head_g, p.H - 1)] * LOG2E, l, m_fin);
+            o_scale = __builtin_amdgcn_exp2f(m_head - m_fin);
+        }
     // (a cut list: NaN outputs, never a silently truncated attention)
-    const float inv = truncated ? __builtin_nanf("") : (has ? (nchunks == 1 && ntiles == 1 ? 1.0f : 1.0f / l) : 0.0f);
+    const float inv =
+        truncated ? __builtin_nanf("") : (has ? (nchunks == 1 && ntiles == 1 ? 1.0f : o_scale / l) : 0.0f);
     const int64_t qrow = (int64_t)b * p.s_q + t;
     const bool to_part = p.part_o != nullptr;
     const int64_t part_row = (int64_t)split * p.B * p.s_q + qrow;
@@ -2453,14 +2511,18 @@ bool heads_ok(int32_t H, int64_t tokens) {
     return H >= 1 && tokens * head_groups(H) <= INT32_MAX;
 }
 
-// 32-head workgroups (dsa_mla_fwd_narrow_kernel) for bf16 576-value rows in
-// the top-k form: when a query token's 128-head workgroup would be mostly
-// padding heads (H <= 64), or when the 128-head workgroups are too few to
-// occupy the GPU without many splits (fewer than 64).
+// Forward kernel for bf16 rows (576-value rows in the top-k or uniform-split
+// CSR form, V4 512-value rows): 32-head workgroups (dsa_mla_fwd_narrow_kernel)
+// when the 128-head kernel would compute at least 4x padding heads (H <= 32),
+// or could not occupy half the GPU even with its splits (fewer than 128
+// workgroups at wide_splits splits).  Per head and row the 32-head kernel
+// costs about 2.3x the cycles, so it pays only where the 128-head kernel
+// leaves CUs idle or computes mostly padding.
 int narrow_groups(int32_t H) { return (H + NARROW_HEADS - 1) / NARROW_HEADS; }
-bool narrow_path(int fmt, int64_t tokens, int32_t H) {
-    if (fmt != DSA_KV_BF16 || H < 1 || tokens * narrow_groups(H) > INT32_MAX) return false;
-    return H <= 64 || tokens * head_groups(H) < 64;
+bool narrow_path(int fmt, int64_t tokens, int32_t H, int wide_splits) {
+    if ((fmt != DSA_KV_BF16 && fmt != DSA_KV_BF16_D512) || H < 1 || tokens * narrow_groups(H) > INT32_MAX)
+        return false;
+    return H <= 32 || tokens * head_groups(H) * wide_splits < 128;
 }
 
 int auto_splits(int64_t queries, int topk) {
@@ -2475,6 +2537,16 @@ int auto_splits(int64_t queries, int topk) {
     return std::min(ns, DSA_MLA_MAX_SPLITS);
 }
 
+// Split count and kernel of a top-k decode call: the caller's count, or the
+// automatic one for the kernel narrow_path picks.
+int decode_splits(const dsa_mla_decode_args* a, bool* narrow) {
+    const int64_t tokens = (int64_t)a->B * a->s_q;
+    const int wide = a->num_splits ? a->num_splits : auto_splits(tokens * head_groups(a->H), a->topk);
+    *narrow = narrow_path(a->kv_format, tokens, a->H, wide);
+    if (a->num_splits || !*narrow) return wide;
+    return auto_splits(tokens * narrow_groups(a->H), a->topk);
+}
+
 int validate_decode(const dsa_mla_decode_args* a, int* ns_out, int* chunk_out) {
     if (!a) return DSA_ERR_NULL_POINTER;
     if (a->B < 0 || a->s_q <= 0 || a->topk < 0 || a->topk > MAX_LIST) return DSA_ERR_BAD_SHAPE;
@@ -2484,9 +2556,8 @@ int validate_decode(const dsa_mla_decode_args* a, int* ns_out, int* chunk_out) {
     if (a->block_table && a->block_size <= 0) return DSA_ERR_BAD_SHAPE;
     if (row_stride_bytes(a->kv_format, a->kv_stride_row) < 0) return DSA_ERR_BAD_STRIDE;
     if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
-    const int64_t tokens = (int64_t)a->B * a->s_q;
-    const int64_t wgs = tokens * (narrow_path(a->kv_format, tokens, a->H) ? narrow_groups(a->H) : head_groups(a->H));
-    const int ns = a->num_splits ? a->num_splits : auto_splits(wgs, a->topk);
+    bool narrow;
+    const int ns = decode_splits(a, &narrow);
     const int chunk = a->topk == 0 ? 0 : (a->topk + ns - 1) / ns;
     if (a->B > 0 && a->topk > 0) {
         if (!a->q || !a->kv_cache || !a->seq_lens || !a->indices || !a->out) return DSA_ERR_NULL_POINTER;
@@ -2512,7 +2583,8 @@ size_t decode_ws_bytes(const dsa_mla_decode_args* a, int ns) {
 
 int launch_fwd(const FwdParams& fp, int fmt, int B, int s_q, int ns, hipStream_t st, bool narrow = false) {
     dim3 grid((unsigned)((int64_t)B * fp.hgroups), s_q, ns), block(NTHR);
-    if (narrow) hipLaunchKernelGGL(dsa_mla_fwd_narrow_kernel, grid, block, 0, st, fp);
+    if (narrow && fmt == DSA_KV_BF16_D512) hipLaunchKernelGGL(dsa_mla_fwd_narrow_kernel<true>, grid, block, 0, st, fp);
+    else if (narrow) hipLaunchKernelGGL(dsa_mla_fwd_narrow_kernel<false>, grid, block, 0, st, fp);
     else if (fmt == DSA_KV_BF16) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_BF16>, grid, block, 0, st, fp);
     else if (fmt == DSA_KV_FP8_656) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_FP8_656>, grid, block, 0, st, fp);
     else if (fmt == DSA_KV_MXFP8) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_MXFP8>, grid, block, 0, st, fp);
@@ -2670,12 +2742,20 @@ size_t mx_ws_bytes(const dsa_mla_decode_mxfp8_args* a, int ns) {
 // least 8 tiles (256 entries of the longest list) per split.  A token's
 // split s covers its list's part s of whole tiles; the partials are merged by
 // the combine kernel (with the attention sink, V4).
+// Split count and kernel of a prefill call (N query tokens, lists of at most
+// max_list entries).
+int prefill_plan(int fmt, int64_t N, int32_t H, int requested, int64_t max_list, bool* narrow);
 int prefill_splits(int requested, int64_t wgs, int64_t max_list) {
     if (requested > 0) return requested;
     if (wgs <= 0 || wgs >= 256) return 1;
     const int64_t want = (256 + wgs - 1) / wgs;
     const int64_t by_len = std::max<int64_t>(1, max_list / 256);
     return (int)std::min<int64_t>(std::min<int64_t>(want, by_len), DSA_MLA_MAX_SPLITS);
+}
+int prefill_plan(int fmt, int64_t N, int32_t H, int requested, int64_t max_list, bool* narrow) {
+    const int wide = prefill_splits(requested, N * head_groups(H), max_list);
+    *narrow = narrow_path(fmt, N, H, wide);
+    return *narrow ? prefill_splits(requested, N * narrow_groups(H), max_list) : wide;
 }
 size_t prefill_ws_bytes(int ns, int64_t N, int H) {
     return ns <= 1 || N == 0 ? 0 : (size_t)ns * N * H * (D_VO + 1) * sizeof(float) + 256;
@@ -2706,9 +2786,8 @@ int validate_prefill(const dsa_mla_prefill_args* a, int* ns_out) {
     if (row_stride_bytes(a->kv_format, a->kv_stride_row) < 0) return DSA_ERR_BAD_STRIDE;
     if (a->topk > MAX_LIST) return DSA_ERR_BAD_SHAPE;
     if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
-    const bool narrow = narrow_path(a->kv_format, a->N, a->H);
-    *ns_out = prefill_splits(a->num_splits, (int64_t)a->N * (narrow ? narrow_groups(a->H) : head_groups(a->H)),
-                             a->topk);
+    bool narrow;
+    *ns_out = prefill_plan(a->kv_format, a->N, a->H, a->num_splits, a->topk, &narrow);
     if (a->N == 0) return DSA_OK;
     if (!a->q || !a->out || (a->topk > 0 && (!a->kv || !a->indices))) return DSA_ERR_NULL_POINTER;
     if ((a->q_stride_n % 8) || (a->q_stride_h % 8) || (a->o_stride_n % 4) || (a->o_stride_h % 4))
@@ -2727,7 +2806,8 @@ int validate_v4(const dsa_mla_prefill_v4_args* a, int* ns_out) {
     if (!heads_ok(a->H, a->N)) return DSA_ERR_BAD_SHAPE;
     if (a->D != DSA_MLA_D_V4) return DSA_ERR_UNSUPPORTED;
     if (a->num_splits < 0 || a->num_splits > DSA_MLA_MAX_SPLITS) return DSA_ERR_BAD_SPLITS;
-    *ns_out = prefill_splits(a->num_splits, (int64_t)a->N * head_groups(a->H), a->max_rows);
+    bool narrow;
+    *ns_out = prefill_plan(DSA_KV_BF16_D512, a->N, a->H, a->num_splits, a->max_rows, &narrow);
     if (a->N == 0) return DSA_OK;
     if (!a->q || !a->out || !a->kv_indptr_prefix || !a->kv_indices_prefix || !a->kv_indptr_extend ||
         !a->kv_indices_extend)
@@ -2845,7 +2925,8 @@ int dsa_mla_decode_noalloc(const dsa_mla_decode_args* a, void* stream) {
 namespace {
 
 int decode_launch(const dsa_mla_decode_args* a, int ns, int chunk, void* ws, hipStream_t st) {
-    const bool narrow = narrow_path(a->kv_format, (int64_t)a->B * a->s_q, a->H);
+    bool narrow;
+    decode_splits(a, &narrow);
     FwdParams fp{};
     fp.H = a->H;
     fp.hgroups = narrow ? narrow_groups(a->H) : head_groups(a->H);
@@ -2913,7 +2994,7 @@ int dsa_mla_decode_csr(const dsa_mla_decode_csr_args* a, void* ws, size_t ws_byt
     if (a->B == 0) return DSA_OK;
     hipStream_t st = (hipStream_t)stream;
     // uniform splits (no work plan) of few query rows or few heads: 32-head workgroups
-    const bool narrow = ns >= 1 && narrow_path(a->kv_format, (int64_t)a->B * a->s_q, a->H);
+    const bool narrow = ns >= 1 && narrow_path(a->kv_format, (int64_t)a->B * a->s_q, a->H, ns);
     FwdParams fp{};
     fp.H = a->H;
     fp.hgroups = narrow ? narrow_groups(a->H) : head_groups(a->H);
@@ -3021,7 +3102,8 @@ int dsa_mla_prefill(const dsa_mla_prefill_args* a, void* ws, size_t ws_bytes, vo
     const size_t need = prefill_ws_bytes(ns, a->N, a->H);
     if (need && (!ws || ws_bytes < need || ((uintptr_t)ws & 15))) return DSA_ERR_WORKSPACE;
     if (a->N == 0) return DSA_OK;
-    const bool narrow = narrow_path(a->kv_format, a->N, a->H);
+    bool narrow;
+    prefill_plan(a->kv_format, a->N, a->H, a->num_splits, a->topk, &narrow);
     FwdParams fp{};
     fp.H = a->H;
     fp.hgroups = narrow ? narrow_groups(a->H) : head_groups(a->H);
@@ -3066,9 +3148,11 @@ int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* a, void* ws, size_t ws_byt
     const size_t need = prefill_ws_bytes(ns, a->N, a->H);
     if (need && (!ws || ws_bytes < need || ((uintptr_t)ws & 15))) return DSA_ERR_WORKSPACE;
     if (a->N == 0) return DSA_OK;
+    bool narrow;
+    prefill_plan(DSA_KV_BF16_D512, a->N, a->H, a->num_splits, a->max_rows, &narrow);
     FwdParams fp{};
     fp.H = a->H;
-    fp.hgroups = head_groups(a->H);
+    fp.hgroups = narrow ? narrow_groups(a->H) : head_groups(a->H);
     fp.q = (const __bf16*)a->q;
     fp.q_sb = a->stride_qo_n; fp.q_st = 0; fp.q_sh = a->stride_qo_h;
     fp.kv = (const unsigned char*)a->unified_kv;
@@ -3084,7 +3168,7 @@ int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* a, void* ws, size_t ws_byt
     fp.lse = a->lse;
     fp.B = a->N; fp.s_q = 1; fp.topk = a->max_rows; fp.chunk = a->max_rows;
     fp.scale_log2 = a->softmax_scale * LOG2E;
-    return prefill_launch(fp, DSA_KV_BF16_D512, ns, a->attn_sink, ws, (hipStream_t)stream);
+    return prefill_launch(fp, DSA_KV_BF16_D512, ns, a->attn_sink, ws, (hipStream_t)stream, narrow);
 }
 
 int dsa_mla_prefill_v4_fp8_workspace_size(const dsa_mla_prefill_v4_fp8_args* a, size_t* bytes) {

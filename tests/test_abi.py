@@ -563,14 +563,20 @@ def test_prefill_split_workspace(lib):
     """Split-K prefill: automatic splits only when fewer than 256 workgroups would run (at
     least 256 list entries per split), the workspace holding num_splits x N x H x 513 floats;
     explicit counts 1..64; a missing or short workspace is rejected before any launch.
-    Workgroups per query: 4 (32-head groups) for bf16 rows with fewer than 64 queries of
-    H = 128, else 1 (128 heads)."""
+    bf16 rows run 32-head workgroups (4 per query at H = 128) when the 128-head ones would
+    number fewer than 128 even split, and then split for those."""
     per = 128 * 513 * 4
     # C5-sized: 8192 queries, unsplit, no workspace
     assert _prefill_ws(lib, lib.dsa_mla_prefill_workspace_size, _prefill_args()) == (0, 0)
-    # 16 queries of a 65536-entry list (64 workgroups of 32 heads): 4 splits
+    # 16 queries of a 65536-entry list: 16 splits (256 workgroups of 128 heads)
     rc, n = _prefill_ws(lib, lib.dsa_mla_prefill_workspace_size, _prefill_args(N=16, topk=65536))
-    assert rc == 0 and n == 4 * 16 * per + 256
+    assert rc == 0 and n == 16 * 16 * per + 256
+    # 16 queries of 2048-entry lists: 8 splits of 128 heads would be 128 workgroups: kept
+    rc, n = _prefill_ws(lib, lib.dsa_mla_prefill_workspace_size, _prefill_args(N=16, topk=2048))
+    assert rc == 0 and n == 8 * 16 * per + 256
+    # 8 queries of 1024: 4 x 8 = 32 workgroups of 128 heads: 32-head groups, 4 splits
+    rc, n = _prefill_ws(lib, lib.dsa_mla_prefill_workspace_size, _prefill_args(N=8, topk=1024))
+    assert rc == 0 and n == 4 * 8 * per + 256
     # 64 queries: 128-head workgroups, 4 splits
     rc, n = _prefill_ws(lib, lib.dsa_mla_prefill_workspace_size, _prefill_args(N=64, topk=65536))
     assert rc == 0 and n == 4 * 64 * per + 256
