@@ -37,9 +37,13 @@
  *
  * Heads.  Every entry takes any head count H >= 1 (H <= 0 is
  * DSA_ERR_BAD_SHAPE).  A query token runs in ceil(H / 128) workgroups of 128
- * heads; the last one computes its heads past H on a copy of head H-1 and
- * stores nothing for them, so outputs, LSEs and partials are written for
- * heads 0..H-1 only.
+ * heads, or, for bf16 rows at H <= 32 or when 128-head workgroups would be
+ * too few to occupy the GPU, in ceil(H / 32) workgroups of 32 heads (the
+ * summation order of the scores then differs, within the same bounds); the
+ * last group computes its heads past H on a copy of head H-1 and stores
+ * nothing for them, so outputs, LSEs and partials are written for heads
+ * 0..H-1 only.  The kernel choice changes dsa_mla_decode_num_splits and the
+ * workspace sizes, which report the split count of the kernel that runs.
  *
  * Numerics.  Scores s = (q . k) * sm_scale in fp32; softmax probabilities are
  * rounded to the P.V product's 16-bit type before it (bf16 for bf16 and MXFP8
@@ -445,11 +449,12 @@ int dsa_mla_prefill_v4(const dsa_mla_prefill_v4_args* args, void* workspace, siz
  *   rope : 64 bf16 values
  * Value d < 448 = float(e4m3(code_d)) * 2^(scale[d / 32] - 127); values
  * 448..511 are the RoPE values (decode_dsa_row_fp8, mla_v4_host.cc:443-453).
- * K = V = the 512-value row; softmax, sink, pools, CSR lists, skipping and
- * LSE, num_splits and the workspace exactly as in dsa_mla_prefill_v4.  Strides in elements of each stream
- * (bytes for nope, bf16 elements for rope and out); nope pointers and strides
- * 16-byte aligned, rope strides multiples of 8, out strides of 4.  The kernel
- * never reads the pad bytes, nor any row the lists do not name.
+ * K = V = the 512-value row; softmax, sink, pools, CSR lists, skipping,
+ * LSE, num_splits and the workspace exactly as in dsa_mla_prefill_v4.
+ * Strides in elements of each stream (bytes for nope, bf16 elements for rope
+ * and out); nope pointers and strides 16-byte aligned, rope strides multiples
+ * of 8, out strides of 4.  The kernel never reads the pad bytes, nor any row
+ * the lists do not name.
  */
 typedef struct {
     const void* q_nope;
