@@ -192,6 +192,21 @@ class DsaError(RuntimeError):
 _LIB = None
 
 
+def bind_torch_hip_runtime() -> None:
+    """Import torch (when installed) before a HIP library of this package is loaded.
+
+    PyTorch-ROCm ships its own libamdhip64 with the soname libamdhip64.so.7, which is also
+    the soname the library links against.  Loaded after torch, the library's dependency
+    resolves to torch's copy: one HIP runtime in the process.  Loaded first, it pulls in
+    /opt/rocm's runtime, torch later loads its own, and the library's launches on torch's
+    memory and streams then fail (DSA_ERR_HIP).  A process without torch has one runtime
+    either way."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def load_library(path: str | None = None) -> ctypes.CDLL:
     """Load libdsa_mla.so (built by opfoundry_amd.build); raise if it is absent."""
     global _LIB
@@ -202,6 +217,7 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         raise RuntimeError(
             f"libdsa_mla.so not found at {p}: build it with `python -m opfoundry_amd.build` "
             "(there is no CPU fallback)")
+    bind_torch_hip_runtime()
     lib = ctypes.CDLL(p)
     sz = ctypes.POINTER(ctypes.c_size_t)
     lib.dsa_mla_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeArgs), sz]
