@@ -986,6 +986,71 @@ def cpu_baseline_prefill(p, sample_queries, total_pairs):
                        f"full step would take {dt * total_pairs / pairs:.0f} s")
 
 
+# ------------------------------------------------------------- gather floor
+
+def gather_floor(args, dev):
+    """The memory floor of the c3 step: libdsa_gather_floor.so moves each query token's 2048
+    656-B rows into LDS with the forward kernel's LDS-DMA loads and tile ring, and computes
+    nothing.  The three input sets' row lists (block table applied) alternate step by step as
+    in the headline; each launch's per-token word sums are checked against torch's."""
+    import ctypes
+    import torch
+    from opfoundry_amd.abi import bind_torch_hip_runtime
+    from opfoundry_amd.build import PROBE_LIB_PATH
+    if not os.path.exists(PROBE_LIB_PATH):
+        raise RuntimeError(f"{PROBE_LIB_PATH} not built: python -m opfoundry_amd.build")
+    bind_torch_hip_runtime()
+    lib = ctypes.CDLL(PROBE_LIB_PATH)
+    lib.dsa_gather_floor.restype = ctypes.c_int
+    lib.dsa_gather_floor.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    cfg = CONFIGS["c3"]
+    log("building c3 inputs")
+    d = make_decode(cfg, dev)
+    B, s_q, topk = d["idx"].shape
+    ntok, bs, row_bytes = B * s_q, d["block_size"], 656
+    kv = d["kv"]
+    # per-row sums of the 164 32-bit words, then the expected per-token sums of each set
+    words = row_bytes // 4
+    rsum = torch.empty(kv.shape[0], dtype=torch.int64, device=dev)
+    for r0 in range(0, kv.shape[0], 1 << 20):
+        rsum[r0:r0 + (1 << 20)] = kv[r0:r0 + (1 << 20)].view(torch.int32).view(-1, words).long().sum(1)
+    sets = []
+    for _, idx in d["sets"]:
+        assert bool((idx >= 0).all()), "c3 lists hold no padding"
+        j = idx.long().view(B, s_q * topk)
+        phys = torch.gather(d["block_table"].long(), 1, j // bs) * bs + j % bs
+        rows = phys.view(ntok, topk).to(torch.int32).contiguous()
+        sets.append((rows, rsum[rows.long()].sum(1) & 0xFFFFFFFF))
+    sums = torch.zeros(ntok, dtype=torch.int32, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    row_bytes_step = ntok * topk * row_bytes
+    out = {"probe": "gather_floor", "workload": "c3", "tokens": ntok, "rows_per_token": topk,
+           "row_bytes": row_bytes, "row_bytes_per_step": row_bytes_step, "results": []}
+    for slots in (2, 3, 4):
+        turn = [0]
+
+        def step():
+            rows = sets[turn[0]][0]
+            rc = lib.dsa_gather_floor(kv.data_ptr(), rows.data_ptr(), ntok, topk, row_bytes, slots,
+                                      sums.data_ptr(), st)
+            if rc:
+                raise RuntimeError(f"dsa_gather_floor returned {rc}")
+            turn[0] = (turn[0] + 1) % len(sets)
+        ok = True
+        for k in range(len(sets)):      # one checked launch per set
+            turn[0] = k
+            step()
+            torch.cuda.synchronize()
+            ok = ok and bool(torch.equal(sums.long() & 0xFFFFFFFF, sets[k][1]))
+        turn[0] = 0
+        log(f"gather floor: {slots} tiles in LDS, checksums {'ok' if ok else 'WRONG'}")
+        ms = time_steps(step, args.steps, args.warmup)
+        out["results"].append({"slots": slots, "us_per_step": ms * 1e3, "checksums_ok": ok,
+                               "row_TBps": row_bytes_step / (ms * 1e-3) / 1e12})
+    return out
+
+
 # --------------------------------------------------------------------- main
 
 def main():
@@ -1019,6 +1084,9 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead: run --steps plain device copies of MIB MiB (the reference "
                          "kernel that scales rocprof FETCH_SIZE / WRITE_SIZE readings)")
+    ap.add_argument("--gather-floor", action="store_true",
+                    help="instead: time the gather-only probe (libdsa_gather_floor.so) on the "
+                         "c3 step's rows, 2, 3 and 4 tiles in LDS")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -1038,6 +1106,9 @@ def main():
         ms = time_steps(lambda: dst.copy_(src), args.steps, args.warmup)
         print(json.dumps({"copy_bytes": n, "ms_per_copy": ms,
                           "GBps_read_plus_write": 2 * n / (ms * 1e-3) / 1e9}))
+        return
+    if args.gather_floor:
+        print(json.dumps(gather_floor(args, dev)))
         return
     if cfg["kind"] == "v4":
         if not args.kernel_only:

@@ -1,8 +1,9 @@
-"""Build libdsa_mla.so (gfx950) in-tree with hipcc.
+"""Build libdsa_mla.so (gfx950) in-tree with hipcc, and beside it the
+measurement probe libdsa_gather_floor.so (bench.py --gather-floor).
 
     python -m opfoundry_amd.build [--verbose]
 
-The shared object lands in opfoundry_amd/_build/ so it travels with the
+The shared objects land in opfoundry_amd/_build/ so they travel with the
 source tree; nothing is installed.
 """
 from __future__ import annotations
@@ -16,6 +17,8 @@ from .abi import LIB_PATH, PKG_DIR
 
 SRC = os.path.join(PKG_DIR, "csrc", "dsa_mla.hip")
 SRCS = [SRC, os.path.join(PKG_DIR, "csrc", "dsa_topk.hip"), os.path.join(PKG_DIR, "csrc", "dsa_indexer.hip")]
+PROBE_SRC = os.path.join(PKG_DIR, "csrc", "dsa_gather_floor.hip")
+PROBE_LIB_PATH = os.path.join(os.path.dirname(LIB_PATH), "libdsa_gather_floor.so")
 INCLUDE = os.path.normpath(os.path.join(PKG_DIR, "..", "include"))
 
 # Packed-fp32 VALU ops are disabled for all device code: only ordinary
@@ -39,10 +42,10 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libdsa_mla.so)")
 
 
-def build(verbose: bool = False, extra_flags: list[str] | None = None) -> str:
-    os.makedirs(os.path.dirname(LIB_PATH), exist_ok=True)
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, *(extra_flags or []), f"-I{INCLUDE}", *SRCS, "-o", tmp]
+def _compile(srcs: list[str], lib: str, verbose: bool, extra_flags: list[str] | None) -> str:
+    os.makedirs(os.path.dirname(lib), exist_ok=True)
+    tmp = lib + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, *(extra_flags or []), f"-I{INCLUDE}", *srcs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -52,8 +55,14 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None) -> str:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{out}")
     if verbose and out.strip():
         print(out)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, lib)
+    return lib
+
+
+def build(verbose: bool = False, extra_flags: list[str] | None = None) -> str:
+    """Compile libdsa_mla.so and the gather-floor probe; return the library's path."""
+    _compile([PROBE_SRC], PROBE_LIB_PATH, verbose, extra_flags)
+    return _compile(SRCS, LIB_PATH, verbose, extra_flags)
 
 
 if __name__ == "__main__":
