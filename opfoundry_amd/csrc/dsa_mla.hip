@@ -200,6 +200,21 @@ __host__ __device__ inline int plan_item_slot(int w) { return (w & (PLAN_LAST - 
 // max_kv_len it was built for
 constexpr int PLAN_HDR_B = 3, PLAN_HDR_SQ = 4, PLAN_HDR_MAXLEN = 5;
 
+// A global-memory pointer from its address (a generic pointer of unknown
+// origin would be accessed with flat loads).
+template <class T>
+__device__ __forceinline__ T* gptr(uintptr_t u) {
+    return (T*)(__attribute__((address_space(1))) T*)u;
+}
+
+// A wave-uniform int32 read through the scalar cache (the constant address
+// space: an s_load, counted apart from the vector loads, so that waiting for it
+// does not wait for vector loads issued earlier).  For data the kernel
+// reading it never writes (the call's index arrays and lengths).
+__device__ __forceinline__ int32_t sload(const int32_t* ptr) {
+    return *(const __attribute__((address_space(4))) int32_t*)(uintptr_t)ptr;
+}
+
 // Inclusive prefix sum over the wave's lanes of v (0 <= v < 16): from the
 // ballots of v's four bits, each counted below the lane (v_mbcnt), with no
 // LDS round trip.
@@ -213,34 +228,45 @@ __device__ __forceinline__ int wave_incl_sum16(int v) {
     return excl + v;
 }
 
-// Physical cache rows of top-k entries jv of query b (-1 where skipped): the
-// block-table reads of all N entries are issued before any is waited for
-// (one memory round trip, not N).
+// Physical cache rows of top-k entries jv of query b (-1 where skipped), in
+// two stages so that a caller can issue other loads between them.
+// topk_ents: paged, the block-table entry of each entry's block (-1 for a
+// skipped entry; a negative table entry is skipped as well, its rows are
+// below 0), all N reads issued before any is waited for (one memory round
+// trip, not N); flat, the entry's block index (-1: skipped).
 template <int N>
-__device__ __forceinline__ void topk_rows(const FwdParams& p, int b, int64_t jmax, const int32_t (&jv)[N],
-                                          int32_t (&rows)[N]) {
-    const int64_t flat = (int64_t)b * p.kv_batch_stride;
+__device__ __forceinline__ void topk_ents(const FwdParams& p, int b, int64_t jmax, const int32_t (&jv)[N],
+                                          int32_t (&ent)[N]) {
     if (p.block_table) {
         const int32_t* bt = p.block_table + (int64_t)b * p.bt_stride;
-        // the block-table entry of each entry's block, -1 for a skipped entry
-        // (a negative entry is skipped as well: its rows are below 0)
-        int32_t ent[N];
 #pragma unroll
         for (int e = 0; e < N; ++e) {
             const int32_t blk = dsa_rows::topk_block(jv[e], jmax, p.block_size, p.bs_shift);
             ent[e] = blk >= 0 ? bt[blk] : -1;
         }
-#pragma unroll
-        for (int e = 0; e < N; ++e)
-            rows[e] = ent[e] < 0 ? -1
-                                 : (int32_t)dsa_rows::topk_finish(jv[e], 0, ent[e], true, p.block_size, p.bs_shift,
-                                                                  flat, p.kv_total_rows);
     } else {
 #pragma unroll
-        for (int e = 0; e < N; ++e)
-            rows[e] = (int32_t)dsa_rows::topk_finish(jv[e], dsa_rows::topk_block(jv[e], jmax, p.block_size, p.bs_shift),
-                                                     0, false, p.block_size, p.bs_shift, flat, p.kv_total_rows);
+        for (int e = 0; e < N; ++e) ent[e] = dsa_rows::topk_block(jv[e], jmax, p.block_size, p.bs_shift);
     }
+}
+// topk_rows_of: the rows, from the entries and what topk_ents gave for them
+template <int N>
+__device__ __forceinline__ void topk_rows_of(const FwdParams& p, int b, const int32_t (&jv)[N],
+                                             const int32_t (&ent)[N], int32_t (&rows)[N]) {
+    const int64_t flat = (int64_t)b * p.kv_batch_stride;
+    const bool paged = p.block_table != nullptr;
+#pragma unroll
+    for (int e = 0; e < N; ++e)
+        rows[e] = ent[e] < 0 ? -1
+                             : (int32_t)dsa_rows::topk_finish(jv[e], 0, paged ? ent[e] : 0, paged, p.block_size,
+                                                              p.bs_shift, flat, p.kv_total_rows);
+}
+template <int N>
+__device__ __forceinline__ void topk_rows(const FwdParams& p, int b, int64_t jmax, const int32_t (&jv)[N],
+                                          int32_t (&rows)[N]) {
+    int32_t ent[N];
+    topk_ents(p, b, jmax, jv, ent);
+    topk_rows_of(p, b, jv, ent, rows);
 }
 
 // One piece of the fp8 dequant in flight: codes + scale, or 16 RoPE bytes.
@@ -443,49 +469,53 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     }
 
     // ---- 0. Q fragments (B operand of S^T = K Q^T): lane -> head r32, k-chunk hi ----
-    // Issued first so their latency overlaps the index resolution below.
+    // Loaded by load_q() once the first index loads are out (section 1): the
+    // loads return in order, so entries and block-table reads issued after Q
+    // would wait for all of Q as well.
     u32x4 qf[L::KS];
     u32x4 q_scales = {0, 0, 0, 0};   // MXFP8: the 16 E8M0 scales of this head's Q
     unsigned q_sc8[2] = {0u, 0u};    // scaled QK^T: the E8M0 bytes of blocks 2 k8 + hi (k8 = 4 i + byte)
-    if constexpr (L::SQK) {
-        // B operand of the scaled fp8 MFMA (64-deep k-steps k8): lane (head,
-        // hi) holds codes 64 k8 + 16 hi .. +15 and 64 k8 + 32 + 16 hi .. +15,
-        // in qf[2 k8] and qf[2 k8 + 1]; RoPE as bf16 in qf[KS_NOPE ..]
-        // (the lane offset from a fresh copy of the lane id: shared with the
-        // epilogue's, it stayed live across the tile loop and spilled)
-        const unsigned char* q8p = p.q8 + (int64_t)b * p.q8_sb + (int64_t)t * p.q8_st + (int64_t)head_q * p.q8_sh +
-                                   16 * (opaque_here(lane) >> 5);
+    auto load_q = [&]() {
+        if constexpr (L::SQK) {
+            // B operand of the scaled fp8 MFMA (64-deep k-steps k8): lane (head,
+            // hi) holds codes 64 k8 + 16 hi .. +15 and 64 k8 + 32 + 16 hi .. +15,
+            // in qf[2 k8] and qf[2 k8 + 1]; RoPE as bf16 in qf[KS_NOPE ..]
+            // (the lane offset from a fresh copy of the lane id: shared with the
+            // epilogue's, it stayed live across the tile loop and spilled)
+            const unsigned char* q8p = p.q8 + (int64_t)b * p.q8_sb + (int64_t)t * p.q8_st + (int64_t)head_q * p.q8_sh +
+                                       16 * (opaque_here(lane) >> 5);
 #pragma unroll
-        for (int k8 = 0; k8 < KS_NOPE / 4; ++k8) {
-            qf[2 * k8] = *reinterpret_cast<const u32x4*>(q8p + 64 * k8);
-            qf[2 * k8 + 1] = *reinterpret_cast<const u32x4*>(q8p + 64 * k8 + 32);
+            for (int k8 = 0; k8 < KS_NOPE / 4; ++k8) {
+                qf[2 * k8] = *reinterpret_cast<const u32x4*>(q8p + 64 * k8);
+                qf[2 * k8 + 1] = *reinterpret_cast<const u32x4*>(q8p + 64 * k8 + 32);
+            }
+            q_scales = *reinterpret_cast<const u32x4*>(p.qsc + (int64_t)b * p.qsc_sb + (int64_t)t * p.qsc_st +
+                                                       (int64_t)head_q * p.qsc_sh);
+            const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head_q * p.q_sh + 8 * hi;
+#pragma unroll
+            for (int ks = KS_NOPE; ks < L::KS; ++ks)
+                qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * (ks - KS_NOPE));
+        } else if constexpr (L::MX) {
+            // fp8 codes of dims 16ks + 8hi .. +7 in the low half of qf[ks],
+            // converted to bf16 once they have landed; RoPE as bf16
+            const unsigned char* q8p = p.q8 + (int64_t)b * p.q8_sb + (int64_t)t * p.q8_st + (int64_t)head_q * p.q8_sh + 8 * hi;
+#pragma unroll
+            for (int ks = 0; ks < L::Q8_KS; ++ks) {
+                const u32x2 c = *reinterpret_cast<const u32x2*>(q8p + 16 * ks);
+                qf[ks] = u32x4{c[0], c[1], 0u, 0u};
+            }
+            q_scales = *reinterpret_cast<const u32x4*>(p.qsc + (int64_t)b * p.qsc_sb + (int64_t)t * p.qsc_st +
+                                                       (int64_t)head_q * p.qsc_sh);
+            const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head_q * p.q_sh + 8 * hi;
+#pragma unroll
+            for (int ks = L::Q8_KS; ks < L::KS; ++ks)
+                qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * (ks - L::Q8_KS));
+        } else {
+            const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head_q * p.q_sh + 8 * hi;
+#pragma unroll
+            for (int ks = 0; ks < L::KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * ks);
         }
-        q_scales = *reinterpret_cast<const u32x4*>(p.qsc + (int64_t)b * p.qsc_sb + (int64_t)t * p.qsc_st +
-                                                   (int64_t)head_q * p.qsc_sh);
-        const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head_q * p.q_sh + 8 * hi;
-#pragma unroll
-        for (int ks = KS_NOPE; ks < L::KS; ++ks)
-            qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * (ks - KS_NOPE));
-    } else if constexpr (L::MX) {
-        // fp8 codes of dims 16ks + 8hi .. +7 in the low half of qf[ks],
-        // converted to bf16 once they have landed; RoPE as bf16
-        const unsigned char* q8p = p.q8 + (int64_t)b * p.q8_sb + (int64_t)t * p.q8_st + (int64_t)head_q * p.q8_sh + 8 * hi;
-#pragma unroll
-        for (int ks = 0; ks < L::Q8_KS; ++ks) {
-            const u32x2 c = *reinterpret_cast<const u32x2*>(q8p + 16 * ks);
-            qf[ks] = u32x4{c[0], c[1], 0u, 0u};
-        }
-        q_scales = *reinterpret_cast<const u32x4*>(p.qsc + (int64_t)b * p.qsc_sb + (int64_t)t * p.qsc_st +
-                                                   (int64_t)head_q * p.qsc_sh);
-        const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head_q * p.q_sh + 8 * hi;
-#pragma unroll
-        for (int ks = L::Q8_KS; ks < L::KS; ++ks)
-            qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * (ks - L::Q8_KS));
-    } else {
-        const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head_q * p.q_sh + 8 * hi;
-#pragma unroll
-        for (int ks = 0; ks < L::KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * ks);
-    }
+    };
 
     // ---- 1. resolve this split's index chunk into a compacted row list ----
     // Top-k form: logical positions through the block table, bounded by
@@ -505,10 +535,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     if (L::D512 && p.ind_pre) {
         // V4: prefix rows of kv, then extend rows of kv2 (tagged with POOL2);
         // a decreasing indptr pair counts as an empty range
-        const int64_t pb = p.ind_pre[b];
-        v4_np = max((int64_t)p.ind_pre[b + 1] - pb, (int64_t)0);
-        v4_eb = p.ind_ext[b];
-        const int64_t ne = max((int64_t)p.ind_ext[b + 1] - v4_eb, (int64_t)0);
+        const int64_t pb = sload(p.ind_pre + b);
+        v4_np = max((int64_t)sload(p.ind_pre + b + 1) - pb, (int64_t)0);
+        v4_eb = sload(p.ind_ext + b);
+        const int64_t ne = max((int64_t)sload(p.ind_ext + b + 1) - v4_eb, (int64_t)0);
         // the token's list (at most max_rows = p.topk entries: a longer one is
         // cut, NaN) split into gridDim.z parts of whole tiles, as the
         // reference's split-K prefill cuts prefix-then-extend rows
@@ -521,8 +551,8 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         k1 = (int)min((int64_t)k0 + cb, n_b);
         idx = p.idx_pre + pb;
     } else if (p.kv_indptr) {
-        const int64_t kb = p.kv_indptr[b];
-        const int64_t count = (int64_t)p.kv_indptr[b + 1] - kb - (p.s_q - 1 - t);
+        const int64_t kb = sload(p.kv_indptr + b);
+        const int64_t count = (int64_t)sload(p.kv_indptr + b + 1) - kb - (p.s_q - 1 - t);
         k1 = (int)min(p.plan_items ? (int64_t)item_k1 : (int64_t)k0 + p.chunk, count);
         truncated = count > k_cap;
         // a row's last item ends at the length the plan was built for: a list
@@ -531,7 +561,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         idx = p.kv_indices + kb;
     } else {
         k1 = (int)min((int64_t)k0 + p.chunk, (int64_t)p.topk);
-        const int64_t Lq = p.seq_lens ? (int64_t)p.seq_lens[b] : p.seq_len_default;
+        const int64_t Lq = p.seq_lens ? (int64_t)sload(p.seq_lens + b) : p.seq_len_default;
         jmax = Lq;
         if (p.causal == 1) jmax = min(Lq, Lq - p.s_q + t + 1);
         else if (p.causal == 2) jmax = min(Lq, (int64_t)b + p.causal_offset + 1);
@@ -543,38 +573,65 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // empty range is one empty chunk.
     const int nchunks = k1 > k0 ? (k1 - k0 + MAX_CHUNK - 1) / MAX_CHUNK : 1;
 
-    // entries [kc0, min(kc0 + MAX_CHUNK, k1)) -> the compacted row list;
-    // sets n_valid and ntiles (ends with a workgroup barrier)
-    int n_valid = 0, ntiles = 0;
-    bool any_rows = false;
-    auto resolve_chunk = [&](int c) {
+    constexpr int PER_T = MAX_CHUNK / NTHR;  // 8 entries per thread and chunk
+    // the entries of chunk c (-1 past the split's end), all loads issued
+    // before any is used; a V4 entry k is an extend entry from k = v4_np on
+    auto load_entries = [&](int c, int32_t (&jv)[PER_T]) {
         const int kc0 = k0 + c * MAX_CHUNK;
         const int kc1 = min(kc0 + MAX_CHUNK, k1);
-        constexpr int PER_T = MAX_CHUNK / NTHR;  // 8 entries per thread
+#pragma unroll
+        for (int e = 0; e < PER_T; ++e) {
+            const int k = kc0 + tid * PER_T + e;
+            if (k >= kc1) jv[e] = -1;
+            else jv[e] = L::D512 && p.ind_pre && k >= v4_np ? p.idx_ext[v4_eb + (k - v4_np)] : idx[k];
+        }
+    };
+    // Chunk 0's entries go out before Q, and a paged top-k list's block-table
+    // reads for them as well (both are waited for before the rows are formed,
+    // which then does not wait for Q); a flat list's rows need no second read.
+    // The first tiles' gathers are then issued while Q is still in flight.
+    int32_t jv0[PER_T], ent0[PER_T];
+    load_entries(0, jv0);
+    const bool topk_paged = !(L::D512 && p.ind_pre) && !p.kv_indptr && p.block_table;
+    if (topk_paged) topk_ents(p, b, jmax, jv0, ent0);
+    load_q();
+
+    // entries [kc0, min(kc0 + MAX_CHUNK, k1)) -> the compacted row list;
+    // sets n_valid and ntiles (ends with a workgroup barrier).  preloaded:
+    // chunk 0 from jv0 / ent0.
+    int n_valid = 0, ntiles = 0;
+    bool any_rows = false;
+    auto resolve_chunk = [&](int c, bool preloaded) {
+        const int kc0 = k0 + c * MAX_CHUNK;
         int32_t rows_local[PER_T];
         int cnt = 0;
         {
-            // all loads first (they overlap), then the rules of dsa_rows.h; a V4
-            // entry is checked against the pool its list names (ext[e])
+            // the rules of dsa_rows.h; a V4 entry is checked against the pool
+            // its list names
             int32_t jv[PER_T];
-            bool ext[PER_T];
+            if (preloaded) {
 #pragma unroll
-            for (int e = 0; e < PER_T; ++e) {
-                const int k = kc0 + tid * PER_T + e;
-                ext[e] = L::D512 && p.ind_pre && k >= v4_np;
-                if (k >= kc1) jv[e] = -1;
-                else jv[e] = ext[e] ? p.idx_ext[v4_eb + (k - v4_np)] : idx[k];
+                for (int e = 0; e < PER_T; ++e) jv[e] = jv0[e];
+            } else {
+                load_entries(c, jv);
             }
             if (L::D512 && p.ind_pre) {
 #pragma unroll
                 for (int e = 0; e < PER_T; ++e)
-                    rows_local[e] = ext[e] ? dsa_rows::v4_extend_row(jv[e], p.kv2_rows)
-                                           : dsa_rows::v4_prefix_row(jv[e], p.kv_total_rows);
+                    rows_local[e] = kc0 + tid * PER_T + e >= v4_np ? dsa_rows::v4_extend_row(jv[e], p.kv2_rows)
+                                                                   : dsa_rows::v4_prefix_row(jv[e], p.kv_total_rows);
             } else if (p.kv_indptr) {
 #pragma unroll
                 for (int e = 0; e < PER_T; ++e) rows_local[e] = dsa_rows::csr_row(jv[e], p.kv_total_rows);
             } else {
-                topk_rows(p, b, jmax, jv, rows_local);
+                int32_t ent[PER_T];
+                if (preloaded && topk_paged) {
+#pragma unroll
+                    for (int e = 0; e < PER_T; ++e) ent[e] = ent0[e];
+                } else {
+                    topk_ents(p, b, jmax, jv, ent);
+                }
+                topk_rows_of(p, b, jv, ent, rows_local);
             }
 #pragma unroll
             for (int e = 0; e < PER_T; ++e) cnt += rows_local[e] >= 0 ? 1 : 0;
@@ -1308,6 +1365,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         __builtin_amdgcn_sched_barrier(0);
     };
 
+    resolve_chunk(0, true);
     for (int pass = 0;; ++pass) {
 #pragma unroll
         for (int mb = 0; mb < D_VO / 32; ++mb) o[mb] = f32x16{};
@@ -1316,17 +1374,21 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         s_max = -INFINITY;
         first_tile = pass == 0;
         for (int c = 0; c < nchunks; ++c) {
-            // a one-chunk list keeps its row list for the second pass
-            if (pass == 0 || nchunks > 1) resolve_chunk(c);
-            // Q and the index loads complete before the gathers are issued: in
-            // the tile loop the only vector-memory loads are the LDS-DMA gathers,
-            // counted explicitly, and the first tile waits for its own rows alone.
-            wait_vm<0>();
-            if (pass == 0 && c == 0) convert_q();
+            // a one-chunk list keeps its row list for the second pass; chunk 0
+            // of pass 0 was resolved before the loop (from jv0 / ent0, which
+            // are then dead in the tile loop)
+            if ((pass == 0 && c > 0) || (pass > 0 && nchunks > 1)) resolve_chunk(c, false);
+            // The first tiles' gathers go out with Q possibly still in flight
+            // (pass 0, chunk 0).  Loads return in order, so the tile loop's
+            // explicit vmcnt waits, which count only gathers, also cover the
+            // older Q loads; the compiler's own waits before Q is used count
+            // only its loads and so wait for these gathers as well.  In the
+            // tile loop the only vector-memory loads are the gathers.
 #pragma unroll
             for (int s = 0; s < NPRE; ++s)
                 if (s < ntiles) issue_rows(load_rows(s), s);
             if (NPRE < ntiles) gnext = load_rows(NPRE);
+            if (pass == 0 && c == 0) convert_q();
             if constexpr (L::SQK) {
                 // Pipelined (MXFP8 V3.2).  Iteration j: QK^T of
                 // tile j; PV of tile j-1 with tile j's softmax numerators and
@@ -1636,21 +1698,6 @@ constexpr int P_BYTES = 2 * 2 * 32 * 16;      // P of a tile: [u][hi][head] x 8 
 __device__ __forceinline__ f32x4 mfma16_bf16(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);
-}
-
-// A global-memory pointer from its address (a generic pointer of unknown
-// origin would be accessed with flat loads).
-template <class T>
-__device__ __forceinline__ T* gptr(uintptr_t u) {
-    return (T*)(__attribute__((address_space(1))) T*)u;
-}
-
-// A wave-uniform int32 read through the scalar cache (the constant address
-// space: an s_load, counted apart from the vector loads, so that waiting for it
-// does not wait for vector loads issued earlier).  For data no kernel of the
-// call writes.
-__device__ __forceinline__ int32_t sload(const int32_t* ptr) {
-    return *(const __attribute__((address_space(4))) int32_t*)(uintptr_t)ptr;
 }
 
 template <bool D512>
