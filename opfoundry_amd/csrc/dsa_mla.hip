@@ -395,6 +395,27 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     LDS_AS int32_t* const s_rows = (LDS_AS int32_t*)s_rows_arr;
     LDS_AS int* const s_misc = (LDS_AS int*)s_misc_arr;
 
+    // Every argument the prologue reads, of every form, loaded in one batch:
+    // an asm statement that takes them as inputs must have them all, so their
+    // scalar loads go out together.  Left to the compiler, each branch below
+    // loaded its fields where it first used them, a chain of about nine
+    // memory round trips before the first list entry was requested.  (Inputs
+    // only, but for Q's address, which the compiler otherwise reloaded in a
+    // round trip of its own just before the Q loads.)
+    const __bf16* q_base = p.q;
+    int64_t q_sb = p.q_sb, q_st = p.q_st, q_sh = p.q_sh;
+    asm volatile("" : "+s"(q_base), "+s"(q_sb), "+s"(q_st), "+s"(q_sh)
+                 : "s"(gridDim.x), "s"(gridDim.z), "s"(p.kv_total_rows),
+                 "s"(p.kv_batch_stride), "s"(p.block_table), "s"(p.bt_stride), "s"(p.block_size),
+                 "s"(p.bs_shift), "s"(p.seq_lens), "s"(p.seq_len_default), "s"(p.indices), "s"(p.idx_sb),
+                 "s"(p.idx_st), "s"(p.kv_indptr), "s"(p.kv_indices), "s"(p.ind_pre), "s"(p.idx_pre),
+                 "s"(p.ind_ext), "s"(p.idx_ext), "s"(p.kv2_rows), "s"(p.B), "s"(p.s_q), "s"(p.topk),
+                 "s"(p.chunk), "s"(p.H), "s"(p.hgroups), "s"(p.plan_items), "s"(p.plan_hdr), "s"(p.causal),
+                 "s"(p.causal_offset), "s"(p.reverse));
+    if constexpr (Lay<FMT>::MX)
+        asm volatile("" ::"s"(p.q8), "s"(p.q8_sb), "s"(p.q8_st), "s"(p.q8_sh), "s"(p.qsc), "s"(p.qsc_sb),
+                     "s"(p.qsc_st), "s"(p.qsc_sh));
+
     // blockIdx.x = work item * hgroups + head group.  A work item is query
     // token b = blockIdx.x, t = blockIdx.y, split blockIdx.z of its list; or,
     // under a CSR plan, an entry of the plan's item table.
@@ -412,10 +433,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         // and max_kv_len.  A plan built for other arguments lays out other
         // items and partial slots: then every query row's outputs are NaN,
         // and nothing else is read or written.
-        const int32_t* hdr = p.plan_hdr;
-        if (__builtin_amdgcn_readfirstlane(hdr[PLAN_HDR_B]) != p.B ||
-            __builtin_amdgcn_readfirstlane(hdr[PLAN_HDR_SQ]) != p.s_q ||
-            __builtin_amdgcn_readfirstlane(hdr[PLAN_HDR_MAXLEN]) != p.chunk) {
+        // (the header's fields are read together, then compared: one round trip)
+        const int32_t hdr_items = sload(p.plan_hdr), hdr_b = sload(p.plan_hdr + PLAN_HDR_B),
+                      hdr_sq = sload(p.plan_hdr + PLAN_HDR_SQ), hdr_len = sload(p.plan_hdr + PLAN_HDR_MAXLEN);
+        if ((hdr_b != p.B) | (hdr_sq != p.s_q) | (hdr_len != p.chunk)) {
             // (the grid holds at least B * s_q workgroups per head group)
             if (gx < p.B * p.s_q) {
                 const int bq = gx / p.s_q, tq = gx - bq * p.s_q;
@@ -443,7 +464,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         }
         // the grid covers the most items a plan can hold: past the plan's
         // count the whole workgroup leaves before any barrier
-        if (item >= __builtin_amdgcn_readfirstlane(p.plan_hdr[0])) return;
+        if (item >= hdr_items) return;
         const int4 w = p.plan_items[item];
         const int qrow_i = __builtin_amdgcn_readfirstlane(w.x);
         if ((unsigned)qrow_i >= (unsigned)(p.B * p.s_q)) return;
@@ -491,7 +512,8 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             }
             q_scales = *reinterpret_cast<const u32x4*>(p.qsc + (int64_t)b * p.qsc_sb + (int64_t)t * p.qsc_st +
                                                        (int64_t)head_q * p.qsc_sh);
-            const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head_q * p.q_sh + 8 * hi;
+            const __bf16* qp = gptr<const __bf16>((uintptr_t)q_base) + (int64_t)b * q_sb + (int64_t)t * q_st +
+                                (int64_t)head_q * q_sh + 8 * hi;
 #pragma unroll
             for (int ks = KS_NOPE; ks < L::KS; ++ks)
                 qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * (ks - KS_NOPE));
@@ -506,12 +528,14 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             }
             q_scales = *reinterpret_cast<const u32x4*>(p.qsc + (int64_t)b * p.qsc_sb + (int64_t)t * p.qsc_st +
                                                        (int64_t)head_q * p.qsc_sh);
-            const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head_q * p.q_sh + 8 * hi;
+            const __bf16* qp = gptr<const __bf16>((uintptr_t)q_base) + (int64_t)b * q_sb + (int64_t)t * q_st +
+                                (int64_t)head_q * q_sh + 8 * hi;
 #pragma unroll
             for (int ks = L::Q8_KS; ks < L::KS; ++ks)
                 qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * (ks - L::Q8_KS));
         } else {
-            const __bf16* qp = p.q + (int64_t)b * p.q_sb + (int64_t)t * p.q_st + (int64_t)head_q * p.q_sh + 8 * hi;
+            const __bf16* qp = gptr<const __bf16>((uintptr_t)q_base) + (int64_t)b * q_sb + (int64_t)t * q_st +
+                                (int64_t)head_q * q_sh + 8 * hi;
 #pragma unroll
             for (int ks = 0; ks < L::KS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 16 * ks);
         }
@@ -561,10 +585,6 @@ dsa_mla_fwd_kernel(const FwdParams p) {
         idx = p.kv_indices + kb;
     } else {
         k1 = (int)min((int64_t)k0 + p.chunk, (int64_t)p.topk);
-        const int64_t Lq = p.seq_lens ? (int64_t)sload(p.seq_lens + b) : p.seq_len_default;
-        jmax = Lq;
-        if (p.causal == 1) jmax = min(Lq, Lq - p.s_q + t + 1);
-        else if (p.causal == 2) jmax = min(Lq, (int64_t)b + p.causal_offset + 1);
         idx = p.indices + (int64_t)b * p.idx_sb + (int64_t)t * p.idx_st;
     }
     // The split's entries are taken MAX_CHUNK at a time (the row list holds
@@ -592,7 +612,16 @@ dsa_mla_fwd_kernel(const FwdParams p) {
     // The first tiles' gathers are then issued while Q is still in flight.
     int32_t jv0[PER_T], ent0[PER_T];
     load_entries(0, jv0);
-    const bool topk_paged = !(L::D512 && p.ind_pre) && !p.kv_indptr && p.block_table;
+    const bool topk_form = !(L::D512 && p.ind_pre) && !p.kv_indptr;
+    if (topk_form) {
+        // the bound on positions, from seq_len and the causal rule (a scalar
+        // load, in flight with the entries)
+        const int64_t Lq = p.seq_lens ? (int64_t)sload(p.seq_lens + b) : p.seq_len_default;
+        jmax = Lq;
+        if (p.causal == 1) jmax = min(Lq, Lq - p.s_q + t + 1);
+        else if (p.causal == 2) jmax = min(Lq, (int64_t)b + p.causal_offset + 1);
+    }
+    const bool topk_paged = topk_form && p.block_table;
     if (topk_paged) topk_ents(p, b, jmax, jv0, ent0);
     load_q();
 
