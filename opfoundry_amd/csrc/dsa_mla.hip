@@ -2379,6 +2379,8 @@ dsa_csr_plan_kernel(const int32_t* __restrict__ indptr, int B, int s_q, int max_
 // m = max(lse_i, sink), den = sum w_i + exp(sink - m), so a sink far above
 // or below every score neither overflows nor underflows.  A row with no
 // attended entry keeps O = 0 and LSE = +inf, as unsplit.
+// splits a wave merges with all its loads in flight at once
+constexpr int SMALL_SPLITS = 16;
 __device__ __forceinline__ void combine_head(const float* __restrict__ part_o, const float* __restrict__ part_lse,
                                              int ns, int64_t first, int64_t step_rows, int row, int head, int H,
                                              int s_q, __bf16* __restrict__ out, int64_t o_sb, int64_t o_st,
@@ -2388,14 +2390,49 @@ __device__ __forceinline__ void combine_head(const float* __restrict__ part_o, c
     const int64_t base = first * H + head;     // partial index of split 0
     const int64_t rh = (int64_t)row * H + head;
     float m = -FLT_MAX;
-    for (int s = lane; s < ns; s += 64) m = fmaxf(m, part_lse[s * stride + base]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    const bool sink_on = sink != nullptr && m > -FLT_MAX;
-    const float sk = sink_on ? sink[head] : 0.0f;
-    if (sink_on) m = fmaxf(m, sk);
     f32x4 acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
     float den = 0.0f;
+    bool sink_on;
+    float sk;
+    if (ns <= SMALL_SPLITS) {
+        // Every split's LSE and O slice loaded at once: one memory round trip
+        // (the general path below needs one for the maximum, then one per
+        // eight splits).  The same maximum and the same sums in split order.
+        float ls[SMALL_SPLITS];
+        f32x4 v[SMALL_SPLITS][2];
+#pragma unroll
+        for (int j = 0; j < SMALL_SPLITS; ++j) {
+            if (j < ns) {
+                ls[j] = part_lse[j * stride + base];
+                const f32x4* src = reinterpret_cast<const f32x4*>(part_o + (j * stride + base) * D_VO + 8 * lane);
+                v[j][0] = src[0];
+                v[j][1] = src[1];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < SMALL_SPLITS; ++j)
+            if (j < ns) m = fmaxf(m, ls[j]);
+        sink_on = sink != nullptr && m > -FLT_MAX;
+        sk = sink_on ? sink[head] : 0.0f;
+        if (sink_on) m = fmaxf(m, sk);
+#pragma unroll
+        for (int j = 0; j < SMALL_SPLITS; ++j) {
+            if (j < ns) {
+                const float w = ls[j] > -FLT_MAX || ls[j] != ls[j] ? __builtin_amdgcn_exp2f((ls[j] - m) * LOG2E) : 0.0f;
+                den += w;
+                acc0 += w * v[j][0];
+                acc1 += w * v[j][1];
+            }
+        }
+        ns = 0;       // (the loop below has nothing left to do)
+    } else {
+        for (int s = lane; s < ns; s += 64) m = fmaxf(m, part_lse[s * stride + base]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        sink_on = sink != nullptr && m > -FLT_MAX;
+        sk = sink_on ? sink[head] : 0.0f;
+        if (sink_on) m = fmaxf(m, sk);
+    }
     // eight splits' loads in flight at a time; sums in split order
     for (int s0 = 0; s0 < ns; s0 += 8) {
         float ls[8];
