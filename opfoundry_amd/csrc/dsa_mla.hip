@@ -1849,8 +1849,22 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
     };
     // Chunk 0's entries are loaded before Q: vmcnt counts in order, so the wait
     // for them does not wait for the Q loads as well.
-    int32_t jv0[PER_T];
+    int32_t jv0[PER_T], ent0[PER_T];
     load_entries(0, jv0);
+    // top-k form: the bound on positions, from seq_len and the causal rule
+    // (a scalar load, in flight with the entries)
+    int64_t jmax = 0;
+    const bool topk_form = !D512 && !p.kv_indptr;
+    if (topk_form) {
+        const int64_t Lq = p.seq_lens ? (int64_t)sload(p.seq_lens + b) : p.seq_len_default;
+        jmax = Lq;
+        if (p.causal == 1) jmax = min(Lq, Lq - p.s_q + t + 1);
+        else if (p.causal == 2) jmax = min(Lq, (int64_t)b + p.causal_offset + 1);
+    }
+    // a paged top-k list's block-table reads for those entries go out before
+    // Q as well: waiting for them then does not wait for Q
+    const bool topk_paged = topk_form && p.block_table;
+    if (topk_paged) topk_ents(p, b, jmax, jv0, ent0);
 
     // ---- Q fragments (B operand of S^T = K Q^T): head hq, dims 32 ks + 8 g4 .. +7 ----
     u32x4 qf[NKS];
@@ -1860,18 +1874,6 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
     }
-    // top-k form: the bound on positions, from seq_len and the causal rule
-    // (a scalar load, in flight with the entries and Q)
-    int64_t jmax = 0;
-    if (!D512 && !p.kv_indptr) {
-        const int64_t Lq = p.seq_lens ? (int64_t)sload(p.seq_lens + b) : p.seq_len_default;
-        jmax = Lq;
-        if (p.causal == 1) jmax = min(Lq, Lq - p.s_q + t + 1);
-        else if (p.causal == 2) jmax = min(Lq, (int64_t)b + p.causal_offset + 1);
-    }
-    // chunk 0's entries have landed (the NKS Q loads per lane, issued after
-    // them, may still be in flight)
-    wait_vm<NKS>();
 
     // entries of chunk c -> the compacted row list, the last tile padded with
     // copies of the first valid row (ends with a barrier)
@@ -1898,7 +1900,14 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
 #pragma unroll
                 for (int e = 0; e < PER_T; ++e) rows_local[e] = dsa_rows::csr_row(jv[e], p.kv_total_rows);
             } else {
-                topk_rows(p, b, jmax, jv, rows_local);
+                int32_t ent[PER_T];
+                if (preloaded && topk_paged) {
+#pragma unroll
+                    for (int e = 0; e < PER_T; ++e) ent[e] = ent0[e];
+                } else {
+                    topk_ents(p, b, jmax, jv, ent);
+                }
+                topk_rows_of(p, b, jv, ent, rows_local);
             }
 #pragma unroll
             for (int e = 0; e < PER_T; ++e) cnt += rows_local[e] >= 0 ? 1 : 0;
@@ -2022,6 +2031,11 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
 
     // O^T accumulators: dims 128 wave + 32 m + (0..31) of the 32 heads: o[m]
     f32x16 o[4];
+    // Chunk 0 of pass 0, from the preloaded entries, outside the pass loop: a
+    // call inside it shared its code with the calls that load their entries
+    // just before use, and the compiler's wait for those (vmcnt(0)) then
+    // drained the Q loads on this path too.
+    resolve_chunk(0, true);
     for (int pass = 0;; ++pass) {
 #pragma unroll
         for (int m = 0; m < 4; ++m) o[m] = f32x16{};
@@ -2030,7 +2044,7 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
         first_tile = pass == 0;
         for (int c = 0; c < nchunks; ++c) {
             // a one-chunk list keeps its row list for the second pass
-            if (pass == 0 || nchunks > 1) resolve_chunk(c, pass == 0 && c == 0);
+            if ((pass == 0 && c > 0) || (pass > 0 && nchunks > 1)) resolve_chunk(c, false);
             // The index loads have completed (the row list is built); Q's may
             // still be in flight: they are older than the gathers, so the tile
             // loop's in-order waits for a tile's gathers cover them too.
