@@ -2482,17 +2482,22 @@ __device__ __forceinline__ void combine_head(const float* __restrict__ part_o, c
     if (lse && lane == 0) lse[rh] = den > 0.0f || den != den ? m + __builtin_amdgcn_logf(den) * LN2 : INFINITY;
 }
 
+constexpr int COMBINE_MAX_Y = 65535;     // the grid's y extent (HIP's limit is 65536)
+
 // uniform splits: split s of row r is partial row s * rows + r.
-// grid = (rows, ceil(H / 4)), block = 256: one wave per (row, head).
-__global__ void __launch_bounds__(256)
+// grid = (rows, min(H, COMBINE_MAX_Y)), block = 64: one workgroup of one wave
+// per (row, head), so that a low-batch call's few rows still spread over every
+// CU (four heads per workgroup put C1's 256 (row, head) pairs on 64 CUs, each
+// pulling 128 KB of partials through its own memory path).  Past
+// COMBINE_MAX_Y heads a workgroup takes every gridDim.y-th head.
+__global__ void __launch_bounds__(64)
 dsa_mla_combine_kernel(const float* __restrict__ part_o, const float* __restrict__ part_lse, int ns,
                        int rows, int H, int s_q, __bf16* __restrict__ out, int64_t o_sb, int64_t o_st,
                        int64_t o_sh, float* __restrict__ lse, const float* __restrict__ sink) {
     const int row = blockIdx.x;
-    const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
-    if (head >= H) return;
-    combine_head(part_o, part_lse, ns, row, rows, row, head, H, s_q, out, o_sb, o_st, o_sh, lse, sink,
-                 threadIdx.x & 63);
+    for (int head = blockIdx.y; head < H; head += gridDim.y)
+        combine_head(part_o, part_lse, ns, row, rows, row, head, H, s_q, out, o_sb, o_st, o_sh, lse, sink,
+                     threadIdx.x & 63);
 }
 
 // The split rows of a CSR work plan: map[i] = (query row, first partial row,
@@ -2723,7 +2728,7 @@ int launch_fwd(const FwdParams& fp, int fmt, int B, int s_q, int ns, hipStream_t
 int launch_combine(const float* po, const float* pl, int ns, int rows, int H, int s_q, void* out, int64_t o_sb,
                    int64_t o_st, int64_t o_sh, float* lse, hipStream_t st, const float* sink = nullptr) {
     if (rows == 0) return DSA_OK;
-    dim3 grid(rows, (H + 3) / 4), block(256);
+    dim3 grid(rows, std::min(H, COMBINE_MAX_Y)), block(64);
     hipLaunchKernelGGL(dsa_mla_combine_kernel, grid, block, 0, st, po, pl, ns, rows, H, s_q, (__bf16*)out, o_sb,
                        o_st, o_sh, lse, sink);
     return hipGetLastError() == hipSuccess ? DSA_OK : DSA_ERR_HIP;
