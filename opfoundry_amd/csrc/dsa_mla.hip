@@ -2242,7 +2242,7 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
 // Math of mla_reduce (opus_attn/dsa_v32/common/mla_reduce.hpp:6-156):
 // m = max lse_i, w_i = exp(lse_i - m) (0 for an empty split),
 // O = sum w_i O_i / sum w_i, LSE = m + ln sum w_i (+inf when all are empty).
-// grid = (rows, ceil(H / 4)), block = 256.
+// Uniform splits: grid = (rows, min(H, 65535)), block = 64.
 // ---------------------------------------------------------------------------
 // ---------------------------------------------------------------------------
 // CSR work plan: one workgroup of 256 threads, on the device (the host cannot
