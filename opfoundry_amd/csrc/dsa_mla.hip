@@ -1704,8 +1704,9 @@ dsa_mla_fwd_kernel(const FwdParams p) {
 
 // ---------------------------------------------------------------------------
 // Narrow forward kernel (bf16 rows: 576-value rows in the top-k form or the
-// CSR form with uniform splits, or the V4 prefill's 512-value rows): one
-// workgroup per (query token, group of 32 heads, split).
+// CSR form with uniform splits, or the V4 prefill's 512-value rows; 656-B fp8
+// rows in the same forms, dequantised to fp16 tiles): one workgroup per
+// (query token, group of 32 heads, split).
 // For few query tokens (low-batch decode) and small head counts: a 128-head
 // workgroup per token leaves most CUs idle, or computes padding heads, while
 // 32-head groups give 4x the workgroups, each with a quarter of the Q load, of
@@ -1728,19 +1729,33 @@ __device__ __forceinline__ f32x4 mfma16_bf16(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);
 }
+__device__ __forceinline__ f32x4 mfma16_f16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+}
 
-template <bool D512>
+template <int NF>
 __global__ void __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(1, 1)))
 dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
+    // row format: 576-value bf16 rows, 512-value bf16 rows (V4), or 656-B fp8
+    // rows (raw tiles gathered into a ring, dequantised into fp16 tiles; the
+    // NoPE MFMAs run on fp16 operands, as in dsa_mla_fwd_kernel<DSA_KV_FP8_656>)
+    constexpr bool D512 = NF == DSA_KV_BF16_D512;
+    constexpr bool F8 = NF == DSA_KV_FP8_656;
+    static_assert(NF == DSA_KV_BF16 || D512 || F8, "narrow kernel row formats");
     // 32-deep k-steps of QK^T: 16 NoPE + 2 RoPE, or the 16 of a 512-value row
     constexpr int NKS = (D512 ? D_NOPE : D_QK) / 32;
-    __shared__ __attribute__((aligned(1024))) unsigned char s_tiles[3 * TILE_BYTES];
+    // bf16: a ring of three tile buffers; fp8: two fp16 tile buffers and a
+    // ring of three raw slots
+    __shared__ __attribute__((aligned(1024))) unsigned char s_tiles[(F8 ? 2 : 3) * TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) unsigned char s_raw[F8 ? 3 * RAW_STRIDE : 16];
     __shared__ __attribute__((aligned(16))) unsigned char s_p[P_BYTES];
     __shared__ int32_t s_rows_arr[MAX_CHUNK];
     // per-head values of the two row halves: [0] first-tile maxima, [1] one-tile
     // sums, [2] pass maxima, [3] final sums; then the references
     __shared__ float s_red_arr[4 * 2 * NARROW_HEADS + NARROW_HEADS];
-    __shared__ int s_misc_arr[NWAVE + 1];    // [0..3] wave counts, [4] restart flag
+    // [0..3] wave counts, [4] restart flag, [5] (fp8) a scale outside the fp16 path's range
+    __shared__ int s_misc_arr[NWAVE + 2];
     const lds_ptr TB = (lds_ptr)s_tiles;
     const lds_ptr PX = (lds_ptr)s_p;
     LDS_AS int32_t* const s_rows = (LDS_AS int32_t*)s_rows_arr;
@@ -1796,7 +1811,10 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
     const int hq = 16 * hb + c16;                 // this lane's head in QK^T and the softmax
     // heads past H are computed on a copy of head H-1 and never stored
     const int head_g = hbase + r32;
-    if (tid == 0) s_misc[NWAVE] = 0;
+    if (tid == 0) {
+        s_misc[NWAVE] = 0;
+        s_misc[NWAVE + 1] = 0;
+    }
 
     // ---- this split's entries, by the rules of dsa_mla_fwd_kernel.  Top-k
     // form: logical positions through the block table, bounded by seq_len and
@@ -1874,6 +1892,40 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qp + 32 * ks);
     }
+    // the softmax scale (log2 units) of this lane's head hq
+    float c_s = p.scale_log2;
+    // fp8 rows, once Q has landed: its NoPE part to fp16 for the fp16 MFMAs.
+    // A head with |q| >= 2^15 would leave fp16's range: the whole head (NoPE
+    // and RoPE) is scaled by 2^-k, bringing its largest NoPE value below
+    // 2^15, and c_s by 2^k, so the scaled scores are the same; both are exact,
+    // and k = 0 for every |q| < 2^15 (as in dsa_mla_fwd_kernel).  A head's
+    // dims are spread over the four lanes g4 of column c16.
+    auto convert_q = [&]() {
+        if constexpr (F8) {
+            typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+            u16x2 amax = {0, 0};
+#pragma unroll
+            for (int ks = 0; ks < KS_NOPE / 2; ++ks)
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    amax = __builtin_elementwise_max(amax, __builtin_bit_cast(u16x2, qf[ks][w] & 0x7FFF7FFFu));
+            // biased exponent of the head's largest |q| (bf16 bits >> 7)
+            int eb = max((int)amax[0], (int)amax[1]) >> 7;
+            eb = max(eb, __shfl_xor(eb, 16, 64));
+            eb = max(eb, __shfl_xor(eb, 32, 64));
+            const int k = max(eb - 141, 0);                   // 141 = 127 + 14
+            const float s = __uint_as_float((unsigned)(127 - k) << 23);
+            c_s = p.scale_log2 * __uint_as_float((unsigned)(127 + k) << 23);
+#pragma unroll
+            for (int ks = 0; ks < KS_NOPE / 2; ++ks)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) qf[ks][w] = bf16x2_to_f16x2(qf[ks][w], s);
+#pragma unroll
+            for (int ks = KS_NOPE / 2; ks < NKS; ++ks)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) qf[ks][w] = bf16x2_scale(qf[ks][w], s);
+        }
+    };
 
     // entries of chunk c -> the compacted row list, the last tile padded with
     // copies of the first valid row (ends with a barrier)
@@ -1948,9 +2000,35 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
         int32_t rope;              // row of this lane's RoPE chunk
     };
     auto slot = [&](int s) -> lds_ptr { return TB + s * TILE_BYTES; };
+    // 656-B rows: the raw tile's 1312 16-byte chunks (rows back to back) are 21
+    // loads, wave w taking loads w, w+4, ... (6 for wave 0, 5 for the others);
+    // lane chunk c16 = 64 k + lane of load k lies in row c16 / 41 of the tile,
+    // at chunk c16 % 41.  Per lane and load: bits 0..15 the byte offset of the
+    // row's id in the row list (row clamped to 31: the last load's spare lanes
+    // read chunks of row 31 into the slot's padding), bits 16..31 the chunk's
+    // byte offset in the row (as in dsa_mla_fwd_kernel).
+    const lds_ptr RAW = (lds_ptr)s_raw;
+    const int my_loads = F8 ? (wave < FP8_LOADS - NWAVE * (FP8_LPW - 1) ? FP8_LPW : FP8_LPW - 1) : 0;
+    uint32_t f_rc[FP8_LPW] = {};
+    if constexpr (F8) {
+#pragma unroll
+        for (int i = 0; i < FP8_LPW; ++i) {
+            const unsigned c16 = 64 * (wave + NWAVE * i) + lane;
+            const unsigned rt = c16 / 41u;
+            f_rc[i] = 4u * (rt < TILE - 1 ? rt : TILE - 1) | (16u * (c16 - 41u * rt)) << 16;
+        }
+    }
     auto load_rows = [&](int ti) -> GatherRows {
         const LDS_AS int32_t* rows = s_rows + ti * TILE;
         GatherRows g;
+        if constexpr (F8) {
+            // (an opaque copy: the unpacked halves would be hoisted out of the loop)
+#pragma unroll
+            for (int i = 0; i < FP8_LPW; ++i)
+                g.r[i] = lds_ld<int32_t>((lds_cptr)rows + ((unsigned)opaque((int)f_rc[i]) & 0xFFFFu));
+            g.rope = 0;
+            return g;
+        }
         const u32x4 ra = lds_ld<u32x4>((lds_cptr)(rows + 8 * wave));
         const u32x4 rv = lds_ld<u32x4>((lds_cptr)(rows + 8 * wave + 4));
 #pragma unroll
@@ -1963,6 +2041,17 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
     };
     auto issue_rows = [&](const GatherRows& g, lds_ptr tb) {
         const int ln = opaque(lane);
+        if constexpr (F8) {
+            // tb: the raw slot
+#pragma unroll
+            for (int i = 0; i < FP8_LPW; ++i)
+                if (i < my_loads) {
+                    const uint64_t row = (uint32_t)g.r[i];
+                    lds_dma16(p.kv + (row * (uint64_t)p.row_bytes + ((unsigned)opaque((int)f_rc[i]) >> 16)),
+                              tb + 1024 * (wave + NWAVE * i));
+                }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < TILE / NWAVE; ++i) {
             const int r = 8 * wave + i;
@@ -1980,7 +2069,57 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
                       tb + ROPE_OFF + 8 * wave * 128);
         }
     };
-    constexpr int LPW = TILE / NWAVE + (D512 ? 0 : 1);     // loads per wave per tile
+    constexpr int LPW = TILE / NWAVE + (D512 ? 0 : 1);     // loads per wave per tile (bf16 rows)
+    // fp8: wait until this wave's loads of all but the newest `keep` tiles landed
+    auto wait_keep = [&](int keep) {
+        if (keep <= 0) wait_vm<0>();
+        else if (keep == 1) {
+            if (my_loads == FP8_LPW) wait_vm<FP8_LPW>();
+            else wait_vm<FP8_LPW - 1>();
+        } else {
+            if (my_loads == FP8_LPW) wait_vm<2 * FP8_LPW>();
+            else wait_vm<2 * (FP8_LPW - 1)>();
+        }
+    };
+    // fp8: raw slot rb -> fp16 tile buffer tb, cooperatively.  Pieces 0..7:
+    // wave w converts row w + 4j, lane l the NoPE codes 8l..8l+7 of scale
+    // group l/16 (fp16 = fp16(code * 2^e) * fp16(mantissa) for scale =
+    // mantissa * 2^e); piece 8: the RoPE values, one 16-byte chunk per thread,
+    // copied as bf16.  A scale at or above FP8_SCALE_LIMIT_BITS sets range_bad
+    // (the outputs then become NaN).  All loads are issued before any store.
+    bool range_bad = false;
+    auto dequant_tile = [&](lds_cptr rb, lds_ptr tb) {
+        const int ln = opaque(lane);
+        u32x2 codes[TILE / NWAVE];
+        unsigned sbits[TILE / NWAVE];
+#pragma unroll
+        for (int j = 0; j < TILE / NWAVE; ++j) {
+            const lds_cptr rr = rb + (wave + NWAVE * j) * FP8_ROW;
+            codes[j] = lds_ld<u32x2>(rr + 8 * ln);
+            sbits[j] = lds_ld<unsigned>(rr + FP8_SCALE_OFF + 4 * (ln >> 4));
+        }
+        const int t8 = opaque(tid);
+        const u32x4 rope = lds_ld<u32x4>(rb + (t8 >> 3) * FP8_ROW + FP8_ROPE_OFF + 16 * (t8 & 7));
+        bool bad = false;
+#pragma unroll
+        for (int j = 0; j < TILE / NWAVE; ++j) {
+            const int r = wave + NWAVE * j;
+            const float sc = __uint_as_float(sbits[j]);
+            bad |= sbits[j] >= FP8_SCALE_LIMIT_BITS;
+            const _Float16 m16 = (_Float16)__uint_as_float((sbits[j] & 0x007FFFFFu) | 0x3F800000u);
+            const f16x2 mm = {m16, m16};
+            const f16x2 h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)codes[j][0], sc, false) * mm;
+            const f16x2 h1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)codes[j][0], sc, true) * mm;
+            const f16x2 h2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)codes[j][1], sc, false) * mm;
+            const f16x2 h3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((int)codes[j][1], sc, true) * mm;
+            const u32x4 out = {__builtin_bit_cast(unsigned, h0), __builtin_bit_cast(unsigned, h1),
+                               __builtin_bit_cast(unsigned, h2), __builtin_bit_cast(unsigned, h3)};
+            lds_st<u32x4>(tb + r * NOPE_STRIDE + 16 * (ln ^ nope_sw(r)), out);
+        }
+        const int rr8 = t8 >> 3, cc8 = t8 & 7;
+        lds_st<u32x4>(tb + ROPE_OFF + 128 * rr8 + 16 * (cc8 ^ rope_sw(rr8)), rope);
+        range_bad |= bad;
+    };
 
     // ---- S^T[16 rows x 16 heads] = K Q^T (A operand: row 16 rb + c16, dims
     // 32 ks + 8 g4 .. +7, i.e. chunk 4 ks + g4 at its swizzled position) ----
@@ -2002,7 +2141,9 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
             __builtin_amdgcn_sched_barrier(0);
-            acc[ks & 1] = mfma16_bf16(kb[ks % KPF], qf[ks], acc[ks & 1]);
+            // (fp8 rows: the NoPE k-steps on fp16 operands, RoPE on bf16)
+            if (F8 && ks < KS_NOPE / 2) acc[ks & 1] = mfma16_f16(kb[ks % KPF], qf[ks], acc[ks & 1]);
+            else acc[ks & 1] = mfma16_bf16(kb[ks % KPF], qf[ks], acc[ks & 1]);
             if (ks + KPF < NKS) kb[ks % KPF] = lds_ld<u32x4>(k_addr(ks + KPF));
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -2011,7 +2152,6 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
 
     // softmax state of head hq over this wave's rows: lane (g4, c16), value i
     // of the 16x16 tile is row 16 rb + 4 g4 + i of the tile
-    const float c_s = p.scale_log2;
     float m_ref = 0.0f, l_lane = 0.0f, s_max = -INFINITY;
     bool first_tile = true;
     // per head over the wave's 16 rows (the 4 lanes g4 of head c16)
@@ -2048,21 +2188,42 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
             // The index loads have completed (the row list is built); Q's may
             // still be in flight: they are older than the gathers, so the tile
             // loop's in-order waits for a tile's gathers cover them too.
-            if (ntiles > 0) issue_rows(load_rows(0), slot(0));
-            if (ntiles > 1) issue_rows(load_rows(1), slot(1));
+            // bf16 rows: tiles 0 and 1 go out before the loop, tile it+2 in
+            // iteration it, into ring slot (it+2) % 3.  fp8 rows: raw tiles 0..2
+            // before the loop, raw tile it+3 in iteration it into raw slot it % 3
+            // (dequantised in iteration it-1); tile j is dequantised into fp16
+            // buffer j % 2 after the PV of tile j-1.
+            constexpr int NPRE = F8 ? 3 : 2;
+            auto ring = [&](int s) -> lds_ptr { return F8 ? RAW + s * RAW_STRIDE : slot(s); };
+#pragma unroll
+            for (int s0 = 0; s0 < NPRE; ++s0)
+                if (s0 < ntiles) issue_rows(load_rows(s0), ring(s0));
             GatherRows gnext;
-            if (ntiles > 2) gnext = load_rows(2);
+            if (NPRE < ntiles) gnext = load_rows(NPRE);
+            if constexpr (F8) {
+                if (pass == 0 && c == 0) convert_q();
+                if (ntiles > 0) {
+                    wait_keep(min(ntiles, NPRE) - 1);    // raw tile 0 landed
+                    tile_barrier();
+                    dequant_tile(RAW, TB);
+                }
+            }
             for (int it = 0; it < ntiles; ++it) {
-                // tile it landed (tile it+1 may be in flight); after the barrier
-                // every wave is done with tile it-1 (its slot receives tile it+2)
-                // and with its P
-                if (it + 1 < ntiles) wait_vm<LPW>();
-                else wait_vm<0>();
+                // bf16: tile it landed (tile it+1 may be in flight); fp8: raw
+                // tile it+1 landed (it+2 may be in flight).  After the barrier
+                // every wave is done with tile it-1 (bf16: its slot receives
+                // tile it+2; fp8: its fp16 buffer receives tile it+1) and with
+                // its P; fp8: tile it's fp16 buffer is complete.
+                if constexpr (F8) {
+                    wait_keep(it + 2 < ntiles ? 1 : 0);
+                } else {
+                    if (it + 1 < ntiles) wait_vm<LPW>();
+                    else wait_vm<0>();
+                }
                 tile_barrier();
-                const lds_ptr kt = slot(it % 3);
-                // the gathers of tile it+2, into the slot of tile it-1
+                const lds_ptr kt = F8 ? TB + (it & 1) * TILE_BYTES : slot(it % 3);
                 __builtin_amdgcn_sched_barrier(0);
-                if (it + 2 < ntiles) issue_rows(gnext, slot((it + 2) % 3));
+                if (it + NPRE < ntiles) issue_rows(gnext, ring((it + NPRE) % 3));
                 __builtin_amdgcn_sched_barrier(0);
                 f32x4 s = qk16(kt);
                 // ---- V^T operands of PV (transposed reads): 16-lane group g16
@@ -2119,17 +2280,31 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
                 l_lane += (e[0] + e[1]) + (e[2] + e[3]);
                 // P of rows 16 rb + 4 g4 + i: PV k-step u = rb, lane half g4 & 1,
                 // positions 4 (g4 >> 1) + i (the rows the V reads pair with them)
-                lds_st<u32x2>(PX + ((2 * rb + (g4 & 1)) * NARROW_HEADS + hq) * 16 + 8 * (g4 >> 1),
-                              __builtin_bit_cast(u32x2, __builtin_convertvector(e, bf16x4)));
+                u32x2 pw;
+                if constexpr (F8) {
+                    // fp16 P for the fp16 PV MFMAs (finite below 2^16: TAU = 15)
+                    const f16x2 p01 = {(_Float16)e[0], (_Float16)e[1]}, p23 = {(_Float16)e[2], (_Float16)e[3]};
+                    pw = u32x2{__builtin_bit_cast(unsigned, p01), __builtin_bit_cast(unsigned, p23)};
+                } else {
+                    pw = __builtin_bit_cast(u32x2, __builtin_convertvector(e, bf16x4));
+                }
+                lds_st<u32x2>(PX + ((2 * rb + (g4 & 1)) * NARROW_HEADS + hq) * 16 + 8 * (g4 >> 1), pw);
                 tile_barrier();
                 // ---- O^T[128 dims of this wave x 32 heads] += V^T P^T ----
 #pragma unroll
                 for (int u = 0; u < 2; ++u) {
                     const u32x4 pb = lds_ld<u32x4>(PX + ((2 * u + vhi) * NARROW_HEADS + (vln & 31)) * 16);
 #pragma unroll
-                    for (int m = 0; m < 4; ++m) o[m] = mfma_bf16(v_frag(u, m), pb, o[m]);
+                    for (int m = 0; m < 4; ++m) {
+                        if constexpr (F8) o[m] = mfma_f16(v_frag(u, m), pb, o[m]);
+                        else o[m] = mfma_bf16(v_frag(u, m), pb, o[m]);
+                    }
                 }
-                if (it + 3 < ntiles) gnext = load_rows(it + 3);
+                // fp8: tile it+1 (landed) into the other fp16 buffer
+                if constexpr (F8)
+                    if (it + 1 < ntiles)
+                        dequant_tile(RAW + ((it + 1) % 3) * RAW_STRIDE, TB + ((it + 1) & 1) * TILE_BYTES);
+                if (it + NPRE + 1 < ntiles) gnext = load_rows(it + NPRE + 1);
             }
             // drain in-flight gathers before the slots can be reused or left
             wait_vm<0>();
@@ -2142,7 +2317,8 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
         // restart refills them, the epilogue stages O in them)
         tile_barrier();
         const float top = get_max(2) * c_s;
-        if (pass == 0 && __builtin_amdgcn_ballot_w64(top - m_ref > Lay<DSA_KV_BF16>::TAU) != 0 && lane == 0)
+        if (pass == 0 && __builtin_amdgcn_ballot_w64(top - m_ref > Lay<F8 ? DSA_KV_FP8_656 : DSA_KV_BF16>::TAU) != 0 &&
+            lane == 0)
             s_misc[NWAVE] = 1;
         tile_barrier();
         if (pass != 0 || s_misc[NWAVE] == 0) break;
@@ -2153,7 +2329,11 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
     // the sums and references per head, from the QK^T lanes to the PV lanes (head r32)
     put_half(3, red4_sum(l_lane));
     if (rb == 0 && g4 == 0) s_red[8 * NARROW_HEADS + hq] = m_ref;
+    if (F8 && range_bad) s_misc[NWAVE + 1] = 1;
     tile_barrier();
+    // A list cut short, or (fp8 rows) a scale outside the fp16 path's range:
+    // NaN outputs, never a silently truncated or wrong attention.
+    const bool nan_out = truncated || (F8 && s_misc[NWAVE + 1] != 0);
     const float l_rows = s_red[6 * NARROW_HEADS + r32] + s_red[7 * NARROW_HEADS + r32];
     const float m_head = s_red[8 * NARROW_HEADS + r32];
     const bool has = any_rows;
@@ -2165,18 +2345,17 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
             add_sink(l_rows, m_head, p.attn_sink[min(head_g, p.H - 1)] * LOG2E, l, m_fin);
             o_scale = __builtin_amdgcn_exp2f(m_head - m_fin);
         }
-    // (a cut list: NaN outputs, never a silently truncated attention)
     const float inv =
-        truncated ? __builtin_nanf("") : (has ? (nchunks == 1 && ntiles == 1 ? 1.0f : o_scale / l) : 0.0f);
+        nan_out ? __builtin_nanf("") : (has ? (nchunks == 1 && ntiles == 1 ? 1.0f : o_scale / l) : 0.0f);
     const int64_t qrow = (int64_t)b * p.s_q + t;
     const bool to_part = p.part_o != nullptr;
     const int64_t part_row = (int64_t)split * p.B * p.s_q + qrow;
     if (wave == 0 && hi == 0 && head_g < p.H) {
-        const float lse_v = truncated ? __builtin_nanf("") : (m_fin + __builtin_amdgcn_logf(l)) * LN2;
+        const float lse_v = nan_out ? __builtin_nanf("") : (m_fin + __builtin_amdgcn_logf(l)) * LN2;
         if (!to_part) {
-            if (p.lse) p.lse[qrow * p.H + head_g] = has || truncated ? lse_v : INFINITY;
+            if (p.lse) p.lse[qrow * p.H + head_g] = has || nan_out ? lse_v : INFINITY;
         } else {
-            p.part_lse[part_row * p.H + head_g] = has || truncated ? lse_v : -FLT_MAX;
+            p.part_lse[part_row * p.H + head_g] = has || nan_out ? lse_v : -FLT_MAX;
         }
     }
     // lane (hi, r32), reg 4g + i of o[m]: dim 128 wave + 32 m + 8 g + 4 hi + i of head r32.
@@ -2644,15 +2823,17 @@ bool heads_ok(int32_t H, int64_t tokens) {
 }
 
 // Forward kernel for bf16 rows (576-value rows in the top-k or uniform-split
-// CSR form, V4 512-value rows): 32-head workgroups (dsa_mla_fwd_narrow_kernel)
-// when the 128-head kernel would compute at least 4x padding heads (H <= 32),
-// or could not occupy half the GPU even with its splits (fewer than 128
-// workgroups at wide_splits splits).  Per head and row the 32-head kernel
-// costs about 2.3x the cycles, so it pays only where the 128-head kernel
-// leaves CUs idle or computes mostly padding.
+// CSR form, V4 512-value rows) and 656-B fp8 rows (the same forms):
+// 32-head workgroups (dsa_mla_fwd_narrow_kernel) when the 128-head kernel
+// would compute at least 4x padding heads (H <= 32), or could not occupy half
+// the GPU even with its splits (fewer than 128 workgroups at wide_splits
+// splits).  Per head and row the 32-head kernel costs about 2.3x the cycles,
+// so it pays only where the 128-head kernel leaves CUs idle or computes
+// mostly padding.
 int narrow_groups(int32_t H) { return (H + NARROW_HEADS - 1) / NARROW_HEADS; }
 bool narrow_path(int fmt, int64_t tokens, int32_t H, int wide_splits) {
-    if ((fmt != DSA_KV_BF16 && fmt != DSA_KV_BF16_D512) || H < 1 || tokens * narrow_groups(H) > INT32_MAX)
+    if ((fmt != DSA_KV_BF16 && fmt != DSA_KV_BF16_D512 && fmt != DSA_KV_FP8_656) || H < 1 ||
+        tokens * narrow_groups(H) > INT32_MAX)
         return false;
     return H <= 32 || tokens * head_groups(H) * wide_splits < 128;
 }
@@ -2715,8 +2896,11 @@ size_t decode_ws_bytes(const dsa_mla_decode_args* a, int ns) {
 
 int launch_fwd(const FwdParams& fp, int fmt, int B, int s_q, int ns, hipStream_t st, bool narrow = false) {
     dim3 grid((unsigned)((int64_t)B * fp.hgroups), s_q, ns), block(NTHR);
-    if (narrow && fmt == DSA_KV_BF16_D512) hipLaunchKernelGGL(dsa_mla_fwd_narrow_kernel<true>, grid, block, 0, st, fp);
-    else if (narrow) hipLaunchKernelGGL(dsa_mla_fwd_narrow_kernel<false>, grid, block, 0, st, fp);
+    if (narrow && fmt == DSA_KV_BF16_D512)
+        hipLaunchKernelGGL(dsa_mla_fwd_narrow_kernel<DSA_KV_BF16_D512>, grid, block, 0, st, fp);
+    else if (narrow && fmt == DSA_KV_FP8_656)
+        hipLaunchKernelGGL(dsa_mla_fwd_narrow_kernel<DSA_KV_FP8_656>, grid, block, 0, st, fp);
+    else if (narrow) hipLaunchKernelGGL(dsa_mla_fwd_narrow_kernel<DSA_KV_BF16>, grid, block, 0, st, fp);
     else if (fmt == DSA_KV_BF16) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_BF16>, grid, block, 0, st, fp);
     else if (fmt == DSA_KV_FP8_656) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_FP8_656>, grid, block, 0, st, fp);
     else if (fmt == DSA_KV_MXFP8) hipLaunchKernelGGL(dsa_mla_fwd_kernel<DSA_KV_MXFP8>, grid, block, 0, st, fp);
