@@ -37,8 +37,9 @@
  *
  * Heads.  Every entry takes any head count H >= 1 (H <= 0 is
  * DSA_ERR_BAD_SHAPE).  A query token runs in ceil(H / 128) workgroups of 128
- * heads, or, for bf16 rows at H <= 32 or when 128-head workgroups would be
- * too few to occupy the GPU, in ceil(H / 32) workgroups of 32 heads (the
+ * heads, or, for bf16 and 656-B fp8 rows at H <= 32 or when 128-head
+ * workgroups would be too few to occupy the GPU, in ceil(H / 32) workgroups
+ * of 32 heads (the
  * summation order of the scores then differs, within the same bounds); the
  * last group computes its heads past H on a copy of head H-1 and stores
  * nothing for them, so outputs, LSEs and partials are written for heads
