@@ -53,6 +53,12 @@ def bf16_fwd_kernel(tokens, splits, heads=H, d512=False):
         return "dsa_mla_fwd_narrow_kernel<" + ("512" if d512 else "576") + ">"
     return "dsa_mla_fwd_kernel<" + ("bf16_d512" if d512 else "bf16") + ">"
 
+def fp8_fwd_kernel(tokens, splits, heads=H):
+    """The same for 656-B fp8 rows (the same selection rule)."""
+    narrow = heads <= 32 or tokens * ((heads + 127) // 128) * splits < 128
+    return "dsa_mla_fwd_narrow_kernel<fp8>" if narrow else "dsa_mla_fwd_kernel<fp8>"
+
+
 CONFIGS = {
     "c1": dict(kind="decode", B=2, s_q=1, seq=8192, block=None, topk=2048, pad=256, fp8=False,
                causal=False),
@@ -1195,6 +1201,10 @@ def main():
     # combine kernel: time the fused kernel alone with per-launch events.
     dom_ms = ms if ns == 1 else kernel_avg_ms(step, max(10, args.steps // 2))
     achieved = alg_bytes / (dom_ms * 1e-3) / 1e9
+    if cfg["fp8"] and not args.no_legs:
+        # the headline's lists (set 0) with fewer heads, the per-GPU head counts of tensor-
+        # parallel DeepSeek-V3.2 serving (128 heads over 8 or 4 GPUs): 32-head workgroups
+        res["decode_heads"] = heads_leg(d, args, dev)
     legs = res
     res = {
         "metric": "sparse-MLA decode us/step + achieved HBM TB/s; prefill TFLOP/s (1 MI355X)",
@@ -1237,6 +1247,41 @@ def main():
         # information only: every roofline fraction is taken against the spec peaks
         res["measured_peaks"] = pk
     print(json.dumps(res))
+
+
+def heads_leg(d, args, dev):
+    """The headline's fp8 lists (set 0: its Q's first H heads, its top-k lists, its cache) at
+    H = 16 and 32.  HBM-bound like the headline: the fraction counts the rows each token
+    attends once, plus Q, O, LSE and the lists of H heads."""
+    import torch
+    from opfoundry_amd import dsa
+    q0, idx0 = d["sets"][0]
+    B, s_q, topk = idx0.shape
+    V = count_valid(d)
+    out = {}
+    for Hs in (16, 32):
+        qh = q0[:, :, :Hs].contiguous()
+        hout = torch.empty((B, s_q, Hs, D_VO), dtype=torch.bfloat16, device=dev)
+        hlse = torch.empty((B, s_q, Hs), dtype=torch.float32, device=dev)
+        a = dsa.make_decode_args(qh, d["kv"], idx0, SM_SCALE, hout, hlse, seq_lens=d["seq_lens"],
+                                 block_table=d["block_table"], block_size=d["block_size"], causal=d["causal"],
+                                 num_splits=0, kv_batch_stride=d["kv_batch_stride"])
+        ns = dsa.decode_num_splits(a)
+        ws = torch.empty(max(dsa.decode_workspace_size(a), 1), dtype=torch.uint8, device=dev)
+        step = prepared_decode([a], ws)
+        ms = time_steps(step, args.steps, args.warmup)
+        alg = (B * s_q * Hs * D_QK * 2 + V * 656 + B * s_q * Hs * D_VO * 2 + B * s_q * Hs * 4
+               + B * s_q * topk * 4)
+        dom_ms = ms if ns == 1 else kernel_avg_ms(step, max(10, args.steps // 2))
+        ach = alg / (dom_ms * 1e-3) / 1e9
+        out[f"H{Hs}"] = {
+            "workload": f"c3 lists (set 0), H={Hs}", "us_per_step": round(ms * 1e3, 3), "num_splits": ns,
+            "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": fp8_fwd_kernel(B * s_q, ns, heads=Hs), "kernel_avg_us": round(dom_ms * 1e3, 3),
+                         "alg_bytes": alg}}
+        del ws, hout, hlse
+    return out
 
 
 def legs_before_headline(args, dev, res):
