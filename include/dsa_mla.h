@@ -115,7 +115,8 @@ enum {
  * kv_cache: [kv_total_rows, row] in kv_format; rows are block_size-row pages,
  *           kv_stride_row elements apart (bf16 elements for DSA_KV_BF16 rows,
  *           bytes for DSA_KV_FP8_656 rows; 0 = dense rows of 576 / 656).  A
- *           row stride is at least one row and a multiple of 16 bytes.
+ *           row stride is at least one row, a multiple of 16 bytes and below
+ *           4 GiB (else DSA_ERR_BAD_STRIDE).
  * out     : bf16 [B, s_q, H, 512] addressed by o_stride_{b,t,h}
  * lse     : fp32 [B, s_q, H] dense (may be NULL)
  * num_splits: 0 = automatic; otherwise 1..DSA_MLA_MAX_SPLITS.  With more than
@@ -218,7 +219,7 @@ int dsa_mla_combine(const float* partial_o, const float* partial_lse, int32_t nu
  *            opus_attn/dsa_v32/README.md:99): bf16 elements for DSA_KV_BF16
  *            rows (the reference harness passes 576), bytes for
  *            DSA_KV_FP8_656 rows; 0 = dense rows.  A row stride is at least
- *            one row and a multiple of 16 bytes.
+ *            one row, a multiple of 16 bytes and below 4 GiB.
  * kv_indptr: int32 [B + 1]; kv_indices: int32 rows.  Query token t of batch b
  *            attends kv_indices[kv_indptr[b] + p] for
  *            0 <= p < kv_indptr[b + 1] - kv_indptr[b] - (s_q - 1 - t)

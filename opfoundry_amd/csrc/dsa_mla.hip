@@ -760,19 +760,25 @@ dsa_mla_fwd_kernel(const FwdParams p) {
             const lds_ptr tb = slot_buf(slot);
             if (i < 8) {
                 const int r = 8 * wave + i;
-                // wave-uniform row: the row address is scalar, the lane part a 32-bit offset
+                // wave-uniform row: the row address is scalar, the lane part a
+                // 32-bit offset.  Row ids are valid (>= 0) and the row stride
+                // is below 4 GiB (checked on the host), so the row's byte
+                // offset is an unsigned 32 x 32-bit product: four scalar
+                // instructions, where a signed 64-bit product takes nine, and
+                // with one wave per SIMD they issue one at a time in the
+                // gather burst after the tile barrier.
                 const unsigned char* base;
                 if constexpr (L::D512) {
                     const int32_t id = g.r[i];
                     base = (dsa_rows::row_in_pool2(id) ? p.kv2 : p.kv) + (int64_t)dsa_rows::row_index(id) * p.row_bytes;
                 } else {
-                    base = p.kv + (int64_t)g.r[i] * p.row_bytes;
+                    base = p.kv + (uint64_t)(uint32_t)g.r[i] * (uint32_t)p.row_bytes;
                 }
                 lds_dma16_s(base, 16u * (unsigned)(ln ^ nope_sw(r)), tb + r * NOPE_STRIDE);
             } else if constexpr (!L::D512) {
                 const int r = 8 * wave + (ln >> 3);
-                const unsigned char* src =
-                    p.kv + (int64_t)g.rope * p.row_bytes + 2 * D_NOPE + 16 * ((ln & 7) ^ rope_sw(r));
+                const unsigned char* src = p.kv + (uint64_t)(uint32_t)g.rope * (uint32_t)p.row_bytes + 2 * D_NOPE +
+                                           16 * ((ln & 7) ^ rope_sw(r));
                 lds_dma16(src, tb + ROPE_OFF + 8 * wave * 128);
             }
         } else {
@@ -2812,7 +2818,8 @@ int64_t row_stride_bytes(int fmt, int64_t stride) {
     const int64_t dense = fmt == DSA_KV_FP8_656 ? FP8_ROW : BF16_ROW;
     if (stride == 0) return dense;
     const int64_t bytes = fmt == DSA_KV_FP8_656 ? stride : 2 * stride;
-    return stride < 0 || bytes < dense || (bytes % 16) != 0 ? -1 : bytes;
+    // (below 4 GiB: the kernels form a row's byte offset as a 32 x 32-bit product)
+    return stride < 0 || bytes < dense || (bytes % 16) != 0 || bytes > 0xFFFFFFF0ll ? -1 : bytes;
 }
 int ilog2(int v) { int s = 0; while ((1 << s) < v) ++s; return s; }
 // workgroups per query token: 128 heads each (the last group masks heads past H)

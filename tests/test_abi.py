@@ -153,6 +153,8 @@ def test_workspace_and_split_plan(lib):
     (dict(kv_stride_row=575), -7), (dict(kv_stride_row=580), -7), (dict(kv_stride_row=-576), -7),
     (dict(kv_format=abi.KV_FP8_656, kv_stride_row=600), -7),
     (dict(kv_format=abi.KV_FP8_656, kv_stride_row=664), -7),
+    # row stride of 4 GiB or more (the kernels form row offsets as 32 x 32-bit products)
+    (dict(kv_stride_row=2 ** 31), -7), (dict(kv_format=abi.KV_FP8_656, kv_stride_row=2 ** 32), -7),
 ])
 def test_decode_rejects_bad_arguments(lib, kw, code):
     a = _decode_args(**kw)
