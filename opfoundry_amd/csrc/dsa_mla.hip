@@ -818,7 +818,7 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                                          : p.kv_sc + row * p.kvs_st);
                     lds_dma16(src, RING + slot * RAW_STRIDE + 1024 * k);
                 } else {
-                    lds_dma16(p.kv + (row * (uint64_t)p.row_bytes + ((unsigned)opaque((int)f_rc[i]) >> 16)),
+                    lds_dma16(p.kv + (row * (uint32_t)p.row_bytes + ((unsigned)opaque((int)f_rc[i]) >> 16)),
                               RING + slot * RAW_STRIDE + 1024 * k);
                 }
             }
@@ -2053,7 +2053,7 @@ dsa_mla_fwd_narrow_kernel(const FwdParams p_arg) {
             for (int i = 0; i < FP8_LPW; ++i)
                 if (i < my_loads) {
                     const uint64_t row = (uint32_t)g.r[i];
-                    lds_dma16(p.kv + (row * (uint64_t)p.row_bytes + ((unsigned)opaque((int)f_rc[i]) >> 16)),
+                    lds_dma16(p.kv + (row * (uint32_t)p.row_bytes + ((unsigned)opaque((int)f_rc[i]) >> 16)),
                               tb + 1024 * (wave + NWAVE * i));
                 }
             return;
