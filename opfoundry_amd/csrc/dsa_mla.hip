@@ -1267,16 +1267,25 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                 return __builtin_bit_cast(u32x4, __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7));
             };
             int step_i = 0;   // MFMA-group counter (8 groups of 4 MFMAs)
+            // P fragments of half u; those of half 1 and its first V fragment
+            // are read in the last MFMA group of half 0
+            u32x4 pbf[NWAVE], pnx[NWAVE];
+#pragma unroll
+            for (int h = 0; h < NWAVE; ++h) pbf[h] = lds_ld<u32x4>(PX + (h * 64 + ln) * 16);
+            u32x4 va_cur = v_frag(0, 0);
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                u32x4 pbf[NWAVE];
-#pragma unroll
-                for (int h = 0; h < NWAVE; ++h) pbf[h] = lds_ld<u32x4>(PX + ((u * NWAVE + h) * 64 + ln) * 16);
-                u32x4 va_cur = v_frag(u, 0);
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
                     __builtin_amdgcn_sched_barrier(0);
-                    const u32x4 va_nxt = m + 1 < 4 ? v_frag(u, m + 1) : va_cur;
+                    u32x4 va_nxt = va_cur;
+                    if (m + 1 < 4) {
+                        va_nxt = v_frag(u, m + 1);
+                    } else if (u == 0) {
+#pragma unroll
+                        for (int h = 0; h < NWAVE; ++h) pnx[h] = lds_ld<u32x4>(PX + ((NWAVE + h) * 64 + ln) * 16);
+                        va_nxt = v_frag(1, 0);
+                    }
 #pragma unroll
                     for (int h = 0; h < NWAVE; ++h) mfma_o<L::F16>(o[4 * m + h], va_cur, pbf[h]);
                     if constexpr (FP8 && !DEQ_QK) {
@@ -1287,6 +1296,10 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                     }
                     va_cur = va_nxt;
                     ++step_i;
+                }
+                if (u == 0) {
+#pragma unroll
+                    for (int h = 0; h < NWAVE; ++h) pbf[h] = pnx[h];
                 }
             }
             if constexpr (FP8 && !DEQ_QK) {
