@@ -1057,6 +1057,54 @@ def gather_floor(args, dev):
     return out
 
 
+# ------------------------------------------------------------- issue probe
+
+ISSUE_MODES = ("4 independent f16 MFMAs per trip (AGPR accumulators)",
+               "+ one 656-B dequant piece after the 4 MFMAs",
+               "+ the same piece split between the single MFMAs",
+               "+ the split piece and its ds_write_b128",
+               "+ 4 v_fma_f32 after every MFMA",
+               "one dependent chain of 36 f16 MFMAs (register operands)",
+               "four interleaved chains of the same 36 MFMAs",
+               "mode 0's MFMAs as compiler builtins (VGPR accumulators)",
+               "mode 0 without the s_nop before each MFMA")
+
+
+def issue_probe(args, dev):
+    """What one wave per SIMD hides under its own MFMAs: libdsa_issue_probe.so runs 256
+    workgroups of 256 threads (one wave per SIMD) through the modes of ISSUE_MODES; each
+    mode's time per trip (4 MFMAs, or 36 for the chain modes) against mode 0's."""
+    import ctypes
+    import torch
+    from opfoundry_amd.abi import bind_torch_hip_runtime
+    from opfoundry_amd.build import ISSUE_PROBE_LIB_PATH
+    if not os.path.exists(ISSUE_PROBE_LIB_PATH):
+        raise RuntimeError(f"{ISSUE_PROBE_LIB_PATH} not built: python -m opfoundry_amd.build")
+    bind_torch_hip_runtime()
+    lib = ctypes.CDLL(ISSUE_PROBE_LIB_PATH)
+    lib.dsa_issue_probe.restype = ctypes.c_int
+    lib.dsa_issue_probe.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    out_buf = torch.empty(256 * 256, dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    res = []
+    for mode, what in enumerate(ISSUE_MODES):
+        chain = mode in (5, 6)
+        iters = 2000 if chain else 20000
+
+        def step():
+            rc = lib.dsa_issue_probe(mode, iters, out_buf.data_ptr(), st)
+            if rc:
+                raise RuntimeError(f"dsa_issue_probe returned {rc}")
+        ms = time_steps(step, 10, 3)
+        mfmas = iters * (36 if chain else 4)
+        res.append({"mode": mode, "what": what, "ns_per_mfma": round(ms * 1e6 / mfmas, 2),
+                    "ms": round(ms, 4)})
+    for r in res:
+        if r["mode"] not in (5, 6):
+            r["vs_mode0"] = round(r["ns_per_mfma"] / res[0]["ns_per_mfma"], 3)
+    return {"probe": "issue", "workgroups": 256, "threads": 256, "results": res}
+
+
 # --------------------------------------------------------------------- main
 
 def main():
@@ -1093,6 +1141,9 @@ def main():
     ap.add_argument("--gather-floor", action="store_true",
                     help="instead: time the gather-only probe (libdsa_gather_floor.so) on the "
                          "c3 step's rows, 2, 3 and 4 tiles in LDS")
+    ap.add_argument("--issue-probe", action="store_true",
+                    help="instead: run the one-wave-per-SIMD issue probe (libdsa_issue_probe.so): "
+                         "which instructions hide under a wave's own MFMAs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -1112,6 +1163,9 @@ def main():
         ms = time_steps(lambda: dst.copy_(src), args.steps, args.warmup)
         print(json.dumps({"copy_bytes": n, "ms_per_copy": ms,
                           "GBps_read_plus_write": 2 * n / (ms * 1e-3) / 1e9}))
+        return
+    if args.issue_probe:
+        print(json.dumps(issue_probe(args, dev)))
         return
     if args.gather_floor:
         print(json.dumps(gather_floor(args, dev)))

@@ -1,5 +1,6 @@
 """Build libdsa_mla.so (gfx950) in-tree with hipcc, and beside it the
-measurement probe libdsa_gather_floor.so (bench.py --gather-floor).
+measurement probes libdsa_gather_floor.so (bench.py --gather-floor) and
+libdsa_issue_probe.so (bench.py --issue-probe).
 
     python -m opfoundry_amd.build [--verbose]
 
@@ -19,6 +20,8 @@ SRC = os.path.join(PKG_DIR, "csrc", "dsa_mla.hip")
 SRCS = [SRC, os.path.join(PKG_DIR, "csrc", "dsa_topk.hip"), os.path.join(PKG_DIR, "csrc", "dsa_indexer.hip")]
 PROBE_SRC = os.path.join(PKG_DIR, "csrc", "dsa_gather_floor.hip")
 PROBE_LIB_PATH = os.path.join(os.path.dirname(LIB_PATH), "libdsa_gather_floor.so")
+ISSUE_PROBE_SRC = os.path.join(PKG_DIR, "csrc", "dsa_issue_probe.hip")
+ISSUE_PROBE_LIB_PATH = os.path.join(os.path.dirname(LIB_PATH), "libdsa_issue_probe.so")
 INCLUDE = os.path.normpath(os.path.join(PKG_DIR, "..", "include"))
 
 # Packed-fp32 VALU ops are disabled for all device code: only ordinary
@@ -60,8 +63,9 @@ def _compile(srcs: list[str], lib: str, verbose: bool, extra_flags: list[str] | 
 
 
 def build(verbose: bool = False, extra_flags: list[str] | None = None) -> str:
-    """Compile libdsa_mla.so and the gather-floor probe; return the library's path."""
+    """Compile libdsa_mla.so and the two measurement probes; return the library's path."""
     _compile([PROBE_SRC], PROBE_LIB_PATH, verbose, extra_flags)
+    _compile([ISSUE_PROBE_SRC], ISSUE_PROBE_LIB_PATH, verbose, extra_flags)
     return _compile(SRCS, LIB_PATH, verbose, extra_flags)
 
 
