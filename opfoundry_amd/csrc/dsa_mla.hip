@@ -767,10 +767,12 @@ dsa_mla_fwd_kernel(const FwdParams p) {
                 // instructions, where a signed 64-bit product takes nine, and
                 // with one wave per SIMD they issue one at a time in the
                 // gather burst after the tile barrier.
+                // (V4 rows: the row stride is 2 x an int32 element count)
                 const unsigned char* base;
                 if constexpr (L::D512) {
                     const int32_t id = g.r[i];
-                    base = (dsa_rows::row_in_pool2(id) ? p.kv2 : p.kv) + (int64_t)dsa_rows::row_index(id) * p.row_bytes;
+                    base = (dsa_rows::row_in_pool2(id) ? p.kv2 : p.kv) +
+                           (uint64_t)(uint32_t)dsa_rows::row_index(id) * (uint32_t)p.row_bytes;
                 } else {
                     base = p.kv + (uint64_t)(uint32_t)g.r[i] * (uint32_t)p.row_bytes;
                 }
